@@ -1,0 +1,348 @@
+// Split-KV GQA decode attention for one query token per sequence.
+//
+// Work unit = (sequence b, kv head, split).  One block of 4 waves owns a
+// contiguous chunk of KV positions of one (b, kv head); its G = H / Hkv query
+// heads share every K/V byte it loads, so K/V cross HBM once per GQA group.
+// Each wave walks 64-position tiles:
+//   * scores S[h, p] = q_h . k_p on MFMA (v_mfma_f32_16x16x32_bf16): A = the
+//     G query rows (zero-padded to 16), B = 16 positions of K per sub-tile;
+//     every lane loads 16-byte pieces of K rows straight into the B operand.
+//   * online softmax in the exp2 domain (scale * log2 e folded into S), with
+//     the running max kept wave-uniform.
+//   * O += P . V on VALU: the 64 V rows are read with fully coalesced 16-byte
+//     loads (one wave instruction covers 1 KiB of consecutive rows); P goes
+//     through a 1 KiB LDS slice per wave and is read back as broadcasts.
+// The 4 waves merge their (max, sum, O) through LDS; with more than one
+// split, the block stores an fp32 partial and the last block of the unit
+// (device-scope arrival counter) merges all splits and writes bf16 output.
+#include "common.h"
+#include "internal.h"
+#include "status.h"
+#include "../../include/ezops_hip.h"
+
+namespace ez {
+namespace {
+
+constexpr int kAttnBlock = 256;
+constexpr int kAttnWaves = 4;
+constexpr int kTile = 64;           // positions per wave iteration
+constexpr int kMinChunk = kTile * kAttnWaves;
+constexpr float kLog2e = 1.4426950408889634f;
+
+int num_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+  }
+  return cus;
+}
+
+struct SplitPlan {
+  int64_t nsplit, chunk;
+};
+
+SplitPlan plan_splits(int64_t B, int64_t Hkv, int64_t S) {
+  const int64_t units = B * Hkv;
+  const int64_t target = int64_t(num_cus()) * 8;
+  int64_t ns = (target + units - 1) / units;
+  const int64_t max_ns = (S + kMinChunk - 1) / kMinChunk;
+  if (ns > max_ns) ns = max_ns;
+  if (ns < 1) ns = 1;
+  int64_t chunk = (S + ns - 1) / ns;
+  chunk = (chunk + kTile - 1) / kTile * kTile;
+  ns = (S + chunk - 1) / chunk;
+  return {ns, chunk};
+}
+
+struct AttnWs {
+  float* opart;   // [B, H, nsplit, D]
+  float* ml;      // [B, H, nsplit, 2]  (max, sum)
+  int* counters;  // [B * Hkv]
+};
+
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+template <int D, int G>
+__global__ __launch_bounds__(kAttnBlock) void attn_split_kernel(AttnArgs a, int64_t nsplit,
+                                                               int64_t chunk, AttnWs ws) {
+  constexpr int NS = D / 32;         // MFMA k-steps per 16-position sub-tile
+  constexpr int CPR = D / 8;         // 16-byte chunks per K/V row
+  constexpr int RPI = kWave / CPR;   // rows covered by one wave-wide V load
+  constexpr int NSUB = kTile / 16;   // MFMA sub-tiles per tile
+  constexpr int NPV = kTile / RPI;   // V rows per lane per tile
+  constexpr int GP = G <= 4 ? 4 : 8; // P row stride in LDS (float4 reads)
+  static_assert(G <= 8, "group size");
+
+  __shared__ __align__(16) float Ps[kAttnWaves][kTile][GP];
+  __shared__ __align__(16) float Os[kAttnWaves][G][D];
+  __shared__ float Ms[kAttnWaves][G], Ls[kAttnWaves][G];
+
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int64_t split = blockIdx.x % nsplit;
+  const int64_t unit = blockIdx.x / nsplit;
+  const int64_t kvh = unit % a.Hkv, b = unit / a.Hkv;
+  int64_t L = a.kv_lens ? int64_t(a.kv_lens[b]) : a.S;
+  L = L < 0 ? 0 : (L > a.S ? a.S : L);
+  const int64_t p_begin = split * chunk;
+  const int64_t p_end = (p_begin + chunk < L) ? p_begin + chunk : L;
+
+  const uint16_t* Kb = a.K + (b * a.Hkv + kvh) * a.S * D;
+  const uint16_t* Vb = a.V + (b * a.Hkv + kvh) * a.S * D;
+  const int64_t h0 = kvh * G;  // first query head of the group
+  const float sl2 = a.scale * kLog2e;
+
+  // Q operand: lane (li, lg) holds Q[h0 + li][lg*(D/4) + 8s .. +8] for step s.
+  bf16x8_t qf[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (li < G) v = *reinterpret_cast<const uint4*>(a.Q + ((b * a.H + h0 + li) * D) + lg * (D / 4) + 8 * s);
+    qf[s] = as_bf16x8(v);
+  }
+
+  float m_run[G], l_acc[G], o[G][8];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    m_run[h] = -INFINITY;
+    l_acc[h] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
+  }
+  const int dc = lane % CPR, rs = lane / CPR;
+
+  for (int64_t t0 = p_begin + int64_t(wave) * kTile; t0 < p_end; t0 += int64_t(kAttnWaves) * kTile) {
+    const int64_t last = p_end - 1;
+    // ---- issue K (MFMA operand layout) and V (row layout) loads
+    uint4 kf[NSUB][NS];
+#pragma unroll
+    for (int u = 0; u < NSUB; ++u) {
+      int64_t p = t0 + 16 * u + li;
+      p = p < last ? p : last;
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+        kf[u][s] = *reinterpret_cast<const uint4*>(Kb + p * D + lg * (D / 4) + 8 * s);
+    }
+    uint4 vf[NPV];
+#pragma unroll
+    for (int j = 0; j < NPV; ++j) {
+      int64_t p = t0 + rs + RPI * j;
+      p = p < last ? p : last;
+      vf[j] = *reinterpret_cast<const uint4*>(Vb + p * D + dc * 8);
+    }
+
+    // ---- scores: acc[u][j] = S[head 4*lg + j][pos t0 + 16u + li]
+    f32x4_t acc[NSUB];
+#pragma unroll
+    for (int u = 0; u < NSUB; ++u) {
+      acc[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+        acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf[s], as_bf16x8(kf[u][s]), acc[u], 0, 0, 0);
+    }
+    float mx[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      mx[j] = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < NSUB; ++u) {
+        const bool ok = t0 + 16 * u + li < p_end;
+        const float sv = ok ? acc[u][j] * sl2 : -INFINITY;
+        acc[u][j] = sv;
+        mx[j] = fmaxf(mx[j], sv);
+      }
+      mx[j] = row16_max(mx[j]);
+    }
+    // ---- wave-uniform running max and rescale factors
+    float m_use[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float mt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx[h & 3]), 16 * (h >> 2)));
+      const float mn = fmaxf(m_run[h], mt);
+      const float alpha = (m_run[h] == -INFINITY) ? 0.f : exp2f(m_run[h] - mn);
+      m_run[h] = mn;
+      m_use[h] = (mn == -INFINITY) ? 0.f : mn;
+      l_acc[h] *= alpha;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[h][e] *= alpha;
+    }
+    // ---- P = exp2(S - m) into LDS as Ps[pos][head]
+    if (lg < GP / 4) {
+#pragma unroll
+      for (int u = 0; u < NSUB; ++u) {
+        float pv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int h = 4 * lg + j;
+          float mu = m_use[j < G ? j : 0];
+          if constexpr (G > 4) mu = (lg == 1) ? m_use[4 + j] : mu;
+          pv[j] = (h < G) ? exp2f(acc[u][j] - mu) : 0.f;
+        }
+        *reinterpret_cast<float4*>(&Ps[wave][16 * u + li][4 * lg]) = make_float4(pv[0], pv[1], pv[2], pv[3]);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // ---- O += P . V
+#pragma unroll
+    for (int j = 0; j < NPV; ++j) {
+      float pr[GP];
+#pragma unroll
+      for (int q4 = 0; q4 < GP / 4; ++q4) {
+        const float4 t = *reinterpret_cast<const float4*>(&Ps[wave][rs + RPI * j][4 * q4]);
+        pr[4 * q4 + 0] = t.x; pr[4 * q4 + 1] = t.y; pr[4 * q4 + 2] = t.z; pr[4 * q4 + 3] = t.w;
+      }
+      float v[8];
+      unpack8(vf[j], v);
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        l_acc[h] += pr[h];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[h][e] = fmaf(pr[h], v[e], o[h][e]);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  // ---- merge the row groups of the wave (lanes with equal dc)
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+#pragma unroll
+    for (int off = CPR; off < kWave; off <<= 1) {
+      l_acc[h] += __shfl_xor(l_acc[h], off, kWave);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[h][e] += __shfl_xor(o[h][e], off, kWave);
+    }
+  }
+  if (rs == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      *reinterpret_cast<float4*>(&Os[wave][h][dc * 8]) = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
+      *reinterpret_cast<float4*>(&Os[wave][h][dc * 8 + 4]) = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      Ms[wave][h] = m_run[h];
+      Ls[wave][h] = l_acc[h];
+    }
+  }
+  __syncthreads();
+
+  // ---- merge the 4 waves: thread handles (h, d) pairs
+  for (int idx = threadIdx.x; idx < G * D; idx += kAttnBlock) {
+    const int h = idx / D, d = idx % D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, Ms[w][h]);
+    float ov = 0.f, lv = 0.f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) {
+      const float f = (Ms[w][h] == -INFINITY) ? 0.f : exp2f(Ms[w][h] - M);
+      ov = fmaf(f, Os[w][h][d], ov);
+      lv = fmaf(f, Ls[w][h], lv);
+    }
+    const int64_t hq = b * a.H + h0 + h;
+    if (nsplit == 1) {
+      a.Out[hq * D + d] = f2bf(lv > 0.f ? ov / lv : 0.f);
+    } else {
+      ws.opart[(hq * nsplit + split) * D + d] = ov;
+      if (d == 0) {
+        ws.ml[(hq * nsplit + split) * 2 + 0] = M;
+        ws.ml[(hq * nsplit + split) * 2 + 1] = lv;
+      }
+    }
+  }
+  if (nsplit == 1) return;
+  if (!arrive_last(ws.counters + unit, int(nsplit))) return;
+
+  // ---- last block of the unit merges the splits
+  for (int idx = threadIdx.x; idx < G * D; idx += kAttnBlock) {
+    const int h = idx / D, d = idx % D;
+    const int64_t hq = b * a.H + h0 + h;
+    const float* ml = ws.ml + hq * nsplit * 2;
+    const float* op = ws.opart + hq * nsplit * D + d;
+    float M = -INFINITY;
+    for (int64_t s = 0; s < nsplit; ++s) M = fmaxf(M, ml[2 * s]);
+    float ov = 0.f, lv = 0.f;
+    for (int64_t s = 0; s < nsplit; ++s) {
+      const float ms = ml[2 * s];
+      const float f = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
+      ov = fmaf(f, op[s * D], ov);
+      lv = fmaf(f, ml[2 * s + 1], lv);
+    }
+    a.Out[hq * D + d] = f2bf(lv > 0.f ? ov / lv : 0.f);
+  }
+}
+
+template <int D>
+void launch_d(const AttnArgs& a, const SplitPlan& pl, const AttnWs& ws, int64_t G, hipStream_t s) {
+  const dim3 grid{unsigned(a.B * a.Hkv * pl.nsplit), 1, 1}, block{kAttnBlock, 1, 1};
+  switch (G) {
+    case 1: hipLaunchKernelGGL((attn_split_kernel<D, 1>), grid, block, 0, s, a, pl.nsplit, pl.chunk, ws); break;
+    case 2: hipLaunchKernelGGL((attn_split_kernel<D, 2>), grid, block, 0, s, a, pl.nsplit, pl.chunk, ws); break;
+    case 4: hipLaunchKernelGGL((attn_split_kernel<D, 4>), grid, block, 0, s, a, pl.nsplit, pl.chunk, ws); break;
+    default: hipLaunchKernelGGL((attn_split_kernel<D, 8>), grid, block, 0, s, a, pl.nsplit, pl.chunk, ws); break;
+  }
+}
+
+}  // namespace
+
+size_t attn_workspace_size(int64_t B, int64_t H, int64_t Hkv, int64_t S, int64_t D) {
+  if (B < 1 || H < 1 || Hkv < 1 || S < 1 || D < 1) return 0;
+  const SplitPlan pl = plan_splits(B, Hkv, S);
+  return align256(size_t(B * H * pl.nsplit * D) * 4) + align256(size_t(B * H * pl.nsplit * 2) * 4) +
+         align256(size_t(B * Hkv) * 4);
+}
+
+int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
+  EZ_REQUIRE(a.Q && a.K && a.V && a.Out, "attn_decode: null pointer");
+  EZ_REQUIRE(a.B >= 1 && a.H >= 1 && a.Hkv >= 1 && a.S >= 1, "attn_decode: bad shape");
+  EZ_REQUIRE(a.H % a.Hkv == 0, "attn_decode: num_heads must be divisible by num_kv_heads");
+  const int64_t G = a.H / a.Hkv;
+  EZ_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "attn_decode: group size %lld not in {1,2,4,8}", (long long)G);
+  EZ_REQUIRE(a.D == 64 || a.D == 128, "attn_decode: head_dim must be 64 or 128");
+  const SplitPlan pl = plan_splits(a.B, a.Hkv, a.S);
+  AttnWs w{};
+  if (pl.nsplit > 1) {
+    EZ_REQUIRE(ws && ws_bytes >= attn_workspace_size(a.B, a.H, a.Hkv, a.S, a.D),
+               "attn_decode: workspace too small (%zu < %zu)", ws_bytes,
+               attn_workspace_size(a.B, a.H, a.Hkv, a.S, a.D));
+    char* p = static_cast<char*>(ws);
+    w.opart = reinterpret_cast<float*>(p);
+    p += align256(size_t(a.B * a.H * pl.nsplit * a.D) * 4);
+    w.ml = reinterpret_cast<float*>(p);
+    p += align256(size_t(a.B * a.H * pl.nsplit * 2) * 4);
+    w.counters = reinterpret_cast<int*>(p);
+  }
+  AttnArgs aa = a;
+  if (aa.scale <= 0.f) aa.scale = 1.0f / sqrtf(float(a.D));
+  if (a.D == 64) launch_d<64>(aa, pl, w, G, s);
+  else launch_d<128>(aa, pl, w, G, s);
+  return launch_status("attn_decode");
+}
+
+}  // namespace ez
+
+extern "C" size_t ezops_attn_decode_workspace_size(int64_t B, int64_t H, int64_t Hkv, int64_t S, int64_t D) {
+  return ez::attn_workspace_size(B, H, Hkv, S, D);
+}
+
+extern "C" int ezops_attn_decode_bf16(const void* Q, const void* K, const void* V, void* Out, int64_t B,
+                                      int64_t H, int64_t Hkv, int64_t S, int64_t D, const int32_t* kv_lens,
+                                      float scale, void* ws, size_t ws_bytes, hipStream_t stream) {
+  ez::AttnArgs a{};
+  a.Q = static_cast<const uint16_t*>(Q);
+  a.K = static_cast<const uint16_t*>(K);
+  a.V = static_cast<const uint16_t*>(V);
+  a.Out = static_cast<uint16_t*>(Out);
+  a.B = B; a.H = H; a.Hkv = Hkv; a.S = S; a.D = D;
+  a.kv_lens = kv_lens;
+  a.scale = scale;
+  return ez::launch_attn(a, ws, ws_bytes, stream);
+}

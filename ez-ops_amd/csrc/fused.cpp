@@ -1,0 +1,153 @@
+// Host-side composition of the fused decode ops from the kernels of
+// gemv.hip, qk_rope.hip and attn.hip, all enqueued on the caller's stream.
+//
+//   o_proj + FFN:  x2 = residual + attn.Wo^T         (linear, residual epilogue)
+//                  h  = silu(n(x2).Wg^T) * n(x2).Wu^T (linear, RMSNorm prologue,
+//                                                       SwiGLU epilogue)
+//                  out = x2 + h.Wd^T                 (linear, residual epilogue)
+//   layer:         qkv = n(hidden).Wqkv^T            (linear, RMSNorm prologue)
+//                  q, k-slot, v-slot = qk_norm_rope(qkv)
+//                  attn = gqa_decode(q, K_cache, V_cache)
+//                  out = o_proj + FFN(attn, hidden)
+#include <hip/hip_runtime.h>
+
+#include "internal.h"
+#include "status.h"
+#include "../../include/ezops_hip.h"
+
+namespace ez {
+namespace {
+
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+struct Carve {
+  char* p;
+  template <typename T>
+  T* take(size_t bytes) {
+    T* r = reinterpret_cast<T*>(p);
+    p += align256(bytes);
+    return r;
+  }
+};
+
+size_t ffn_ws(int64_t B, int64_t HS, int64_t IS) {
+  return align256(size_t(B * HS) * 2) + align256(size_t(B * IS) * 2);
+}
+
+int run_ffn(const uint16_t* attn, const uint16_t* residual, const uint16_t* Wo, const uint16_t* post_w,
+            const uint16_t* Wg, const uint16_t* Wu, const uint16_t* Wd, uint16_t* out, int64_t B,
+            int64_t HS, int64_t IS, int64_t QR, float eps, char* ws, hipStream_t s) {
+  Carve c{ws};
+  uint16_t* x2 = c.take<uint16_t>(size_t(B * HS) * 2);
+  uint16_t* h = c.take<uint16_t>(size_t(B * IS) * 2);
+
+  LinearArgs o{};
+  o.X = attn; o.ldx = QR; o.W = Wo; o.Y = x2; o.ldy = HS;
+  o.M = B; o.N = HS; o.K = QR; o.res = residual; o.ldr = HS; o.epi = kEpiResid;
+  int rc = launch_linear(o, s);
+  if (rc) return rc;
+
+  LinearArgs gu{};
+  gu.X = x2; gu.ldx = HS; gu.W = Wg; gu.W2 = Wu; gu.Y = h; gu.ldy = IS;
+  gu.M = B; gu.N = IS; gu.K = HS; gu.norm = 1; gu.norm_w = post_w; gu.eps = eps; gu.epi = kEpiSilu;
+  rc = launch_linear(gu, s);
+  if (rc) return rc;
+
+  LinearArgs dn{};
+  dn.X = h; dn.ldx = IS; dn.W = Wd; dn.Y = out; dn.ldy = HS;
+  dn.M = B; dn.N = HS; dn.K = IS; dn.res = x2; dn.ldr = HS; dn.epi = kEpiResid;
+  return launch_linear(dn, s);
+}
+
+}  // namespace
+}  // namespace ez
+
+using namespace ez;
+
+extern "C" size_t ezops_o_proj_ffn_workspace_size(int64_t B, int64_t HS, int64_t IS, int64_t QR) {
+  (void)QR;
+  return ffn_ws(B, HS, IS);
+}
+
+extern "C" int ezops_o_proj_ffn_bf16(const void* attn, const void* residual, const void* Wo,
+                                     const void* post_norm_w, const void* Wg, const void* Wu,
+                                     const void* Wd, void* out, int64_t B, int64_t HS, int64_t IS,
+                                     int64_t QR, float eps, void* ws, size_t ws_bytes, hipStream_t s) {
+  EZ_REQUIRE(attn && residual && Wo && Wg && Wu && Wd && out && ws, "o_proj_ffn: null pointer");
+  EZ_REQUIRE(B >= 1 && HS >= 1 && IS >= 1 && QR >= 1, "o_proj_ffn: bad shape");
+  EZ_REQUIRE(ws_bytes >= ffn_ws(B, HS, IS), "o_proj_ffn: workspace too small");
+  return run_ffn(static_cast<const uint16_t*>(attn), static_cast<const uint16_t*>(residual),
+                 static_cast<const uint16_t*>(Wo), static_cast<const uint16_t*>(post_norm_w),
+                 static_cast<const uint16_t*>(Wg), static_cast<const uint16_t*>(Wu),
+                 static_cast<const uint16_t*>(Wd), static_cast<uint16_t*>(out), B, HS, IS, QR, eps,
+                 static_cast<char*>(ws), s);
+}
+
+extern "C" size_t ezops_qwen3_layer_workspace_size(const ezops_qwen3_layer* p) {
+  if (!p) return 0;
+  const int64_t QR = p->H * p->D, KVR = p->Hkv * p->D;
+  return align256(size_t(p->B * (QR + 2 * KVR)) * 2)   // qkv
+         + align256(size_t(p->B * QR) * 2)              // normed/rotated q
+         + align256(size_t(p->B * QR) * 2)              // attention output
+         + align256(attn_workspace_size(p->B, p->H, p->Hkv, p->S, p->D)) + ffn_ws(p->B, p->HS, p->IS);
+}
+
+extern "C" int ezops_qwen3_dense_decode_bf16(const ezops_qwen3_layer* p, void* ws, size_t ws_bytes,
+                                             hipStream_t s) {
+  EZ_REQUIRE(p, "qwen3_dense_decode: null parameter block");
+  EZ_REQUIRE(p->hidden && p->K_cache && p->V_cache && p->Wqkv && p->Wo && p->Wgu && p->Wd && p->out && ws,
+             "qwen3_dense_decode: null pointer");
+  EZ_REQUIRE(p->B >= 1 && p->S >= 1 && p->HS >= 1 && p->IS >= 1 && p->H >= 1 && p->Hkv >= 1 && p->D >= 2,
+             "qwen3_dense_decode: bad shape");
+  EZ_REQUIRE(p->H % p->Hkv == 0, "qwen3_dense_decode: num_heads must be divisible by num_kv_heads");
+  EZ_REQUIRE((p->cos == nullptr) == (p->sin == nullptr), "qwen3_dense_decode: cos and sin go together");
+  EZ_REQUIRE(ws_bytes >= ezops_qwen3_layer_workspace_size(p), "qwen3_dense_decode: workspace too small");
+  const int64_t QR = p->H * p->D, KVR = p->Hkv * p->D, QKV = QR + 2 * KVR;
+  Carve c{static_cast<char*>(ws)};
+  uint16_t* qkv = c.take<uint16_t>(size_t(p->B * QKV) * 2);
+  uint16_t* qn = c.take<uint16_t>(size_t(p->B * QR) * 2);
+  uint16_t* att = c.take<uint16_t>(size_t(p->B * QR) * 2);
+  char* attn_ws = c.take<char>(attn_workspace_size(p->B, p->H, p->Hkv, p->S, p->D));
+  char* ffn = c.p;
+
+  const uint16_t* hidden = static_cast<const uint16_t*>(p->hidden);
+  LinearArgs l{};
+  l.X = hidden; l.ldx = p->HS; l.W = static_cast<const uint16_t*>(p->Wqkv); l.Y = qkv; l.ldy = QKV;
+  l.M = p->B; l.N = QKV; l.K = p->HS; l.norm = 1; l.norm_w = static_cast<const uint16_t*>(p->in_norm_w);
+  l.eps = p->eps; l.epi = kEpiStore;
+  int rc = launch_linear(l, s);
+  if (rc) return rc;
+
+  QkRopeArgs r{};
+  r.q = qkv; r.q_bs = QKV;
+  r.k = qkv + QR; r.k_bs = QKV;
+  r.v = qkv + QR + KVR; r.v_bs = QKV;
+  r.qw = static_cast<const uint16_t*>(p->q_norm_w);
+  r.kw = static_cast<const uint16_t*>(p->k_norm_w);
+  r.cos = static_cast<const uint16_t*>(p->cos);
+  r.sin = static_cast<const uint16_t*>(p->sin);
+  r.Kc = static_cast<uint16_t*>(p->K_cache);
+  r.Vc = static_cast<uint16_t*>(p->V_cache);
+  r.q_out = qn; r.k_out = nullptr;
+  r.B = p->B; r.H = p->H; r.Hkv = p->Hkv; r.D = p->D; r.S = p->S;
+  r.position = p->S - 1; r.positions = p->kv_lens; r.pos_offset = p->kv_lens ? -1 : 0;
+  r.eps = p->eps;
+  rc = launch_qk_norm_rope(r, s);
+  if (rc) return rc;
+
+  AttnArgs a{};
+  a.Q = qn;
+  a.K = static_cast<const uint16_t*>(p->K_cache);
+  a.V = static_cast<const uint16_t*>(p->V_cache);
+  a.Out = att;
+  a.B = p->B; a.H = p->H; a.Hkv = p->Hkv; a.S = p->S; a.D = p->D;
+  a.kv_lens = p->kv_lens;
+  a.scale = 0.f;
+  rc = launch_attn(a, attn_ws, attn_workspace_size(p->B, p->H, p->Hkv, p->S, p->D), s);
+  if (rc) return rc;
+
+  const uint16_t* Wgu = static_cast<const uint16_t*>(p->Wgu);
+  return run_ffn(att, hidden, static_cast<const uint16_t*>(p->Wo), static_cast<const uint16_t*>(p->post_norm_w),
+                 Wgu, Wgu + p->IS * p->HS, static_cast<const uint16_t*>(p->Wd), static_cast<uint16_t*>(p->out),
+                 p->B, p->HS, p->IS, QR, p->eps, ffn, s);
+}

@@ -1,0 +1,375 @@
+// bf16 GEMV and skinny linear layers, Y[M, N] = X[M, K] . W[N, K]^T.
+//
+// Decode-time projections are HBM-bound: every weight byte is read once and
+// used M times.  Two kernels cover the batch range:
+//   * gemv_valu (M <= 4): one wave per R weight rows; each lane streams
+//     16-byte (8 x bf16) chunks of the row, so one wave instruction reads a
+//     fully coalesced 1 KiB of the row; fp32 FMAs; one wave reduction per
+//     output.
+//   * linear_mfma (M > 4): v_mfma_f32_16x16x32_bf16 on 16-row weight tiles
+//     against 16 batch rows; the K range is split over the 4 waves of a
+//     block and the partial tiles are summed through LDS.
+// Both can fuse the RMSNorm prologue (statistics from the X chunks already
+// in registers) and the residual / SwiGLU epilogues of the decode layer.
+#include "common.h"
+#include "internal.h"
+#include "status.h"
+#include "../../include/ezops_hip.h"
+
+namespace ez {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kWavesPerBlock = kBlock / kWave;
+
+__device__ __forceinline__ void store_out(const LinearArgs& a, int64_t m, int64_t n, float v,
+                                          float v_up) {
+  if (a.epi == kEpiStoreF32) {
+    reinterpret_cast<float*>(a.Y)[m * a.ldy + n] = v;
+    return;
+  }
+  uint16_t* y = reinterpret_cast<uint16_t*>(a.Y) + m * a.ldy + n;
+  if (a.epi == kEpiStore) {
+    *y = f2bf(v);
+  } else if (a.epi == kEpiResid) {
+    *y = f2bf(bf2f(a.res[m * a.ldr + n]) + round_bf(v));
+  } else {  // kEpiSilu: bf16 staging as silu(gate) * up on bf16 tensors
+    float g = round_bf(v), u = round_bf(v_up);
+    *y = f2bf(round_bf(silu(g)) * u);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// VALU GEMV, M <= 4.  Wave w of block b owns R consecutive weight rows
+// (kEpiSilu: R = 2 with gate row n and up row n).  U chunks per lane are in
+// flight per loop trip.
+template <int M, int R, int U, bool NORM, bool SILU>
+__global__ __launch_bounds__(kBlock) void gemv_valu_kernel(LinearArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t wrow = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  const int64_t n0 = SILU ? wrow : wrow * R;
+  if (n0 >= a.N) return;
+
+  const int64_t nchunk = a.K >> 3;
+  const uint4* wp[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint16_t* base = (SILU && r == 1) ? a.W2 : a.W;
+    int64_t row = SILU ? n0 : n0 + r;
+    if (row >= a.N) row = a.N - 1;  // tail rows: load a valid row, skip the store
+    wp[r] = reinterpret_cast<const uint4*>(base + row * a.K);
+  }
+  const uint4* xp[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) xp[m] = reinterpret_cast<const uint4*>(a.X + m * a.ldx);
+  const uint4* nwp = reinterpret_cast<const uint4*>(a.norm_w);
+
+  float acc[M][R];
+  float ss[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    ss[m] = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[m][r] = 0.f;
+  }
+
+  for (int64_t c0 = lane; c0 < nchunk; c0 += int64_t(kWave) * U) {
+    uint4 wv[U][R], xv[U][M], nv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = c0 + int64_t(kWave) * u;
+      const bool ok = c < nchunk;
+#pragma unroll
+      for (int r = 0; r < R; ++r) wv[u][r] = ok ? wp[r][c] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int m = 0; m < M; ++m) xv[u][m] = ok ? xp[m][c] : make_uint4(0, 0, 0, 0);
+      if (NORM) nv[u] = (ok && nwp) ? nwp[c] : make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float nw[8];
+      if (NORM) unpack8(nv[u], nw);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float x[8];
+        unpack8(xv[u][m], x);
+        if (NORM) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            ss[m] = fmaf(x[e], x[e], ss[m]);
+            x[e] *= nw[e];
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          float w[8];
+          unpack8(wv[u][r], w);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[m][r] = fmaf(w[e], x[e], acc[m][r]);
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    float scale = 1.f;
+    if (NORM) scale = rsqrtf(wave_sum(ss[m]) / float(a.K) + a.eps);
+    float v[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) v[r] = wave_sum(acc[m][r]) * scale;
+    if (lane == 0) {
+      if (SILU) {
+        store_out(a, m, n0, v[0], v[1]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          if (n0 + r < a.N) store_out(a, m, n0 + r, v[r], 0.f);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA skinny GEMM for 16 batch rows (blockIdx.y selects the 16-row batch
+// block).  Block = 4 waves; the block owns T weight tiles of 16 rows and
+// wave w accumulates the w-th quarter of the K range (128-wide chunks).
+//
+// v_mfma_f32_16x16x32_bf16 operands, lane l = 16*g + i (g = l/16, i = l%16):
+//   A (weights):  A[i][g*8 .. g*8+7]   = W[row0 + i][k(g, s, 0..7)]
+//   B (batch):    B[g*8 .. g*8+7][i]   = X[m0 + i][k(g, s, 0..7)]
+//   C:            C[4*g + j][i], j = 0..3  -> weight row row0+4g+j, batch m0+i
+// The k-slot assignment k(g, s, e) = k0 + 32*g + 8*s + e (s = sub-step 0..3
+// of a 128-wide chunk) is the same for A and B, so the contraction is
+// exact, and each lane reads 64 contiguous bytes of its weight row per chunk.
+template <int T, bool NORM, bool SILU>
+__global__ __launch_bounds__(kBlock) void linear_mfma_kernel(LinearArgs a) {
+  __shared__ float red[kWavesPerBlock][T][4][kWave];
+  __shared__ float ssq[kWavesPerBlock][16];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  const int i = lane & 15, g = lane >> 4;
+  const int64_t m0 = int64_t(blockIdx.y) * 16;
+  const int64_t m = m0 + i;
+  const bool mvalid = m < a.M;
+
+  int64_t tile0[T];
+  const uint16_t* wrow[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    tile0[t] = SILU ? int64_t(blockIdx.x) * 16 : (int64_t(blockIdx.x) * T + t) * 16;
+    int64_t row = tile0[t] + i;
+    if (row >= a.N) row = a.N - 1;
+    wrow[t] = ((SILU && t == 1) ? a.W2 : a.W) + row * a.K;
+  }
+  const uint16_t* xrow = a.X + (mvalid ? m : 0) * a.ldx;
+
+  const int64_t nchunks = (a.K + 127) / 128;
+  const int64_t cb = nchunks * wave / kWavesPerBlock, ce = nchunks * (wave + 1) / kWavesPerBlock;
+
+  f32x4_t acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float ss = 0.f;
+
+  for (int64_t c = cb; c < ce; ++c) {
+    const int64_t kb = c * 128 + g * 32;
+    uint4 wv[T][4], xv[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int64_t k = kb + s * 8;
+      const bool ok = k < a.K;
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+        wv[t][s] = ok ? *reinterpret_cast<const uint4*>(wrow[t] + k) : make_uint4(0, 0, 0, 0);
+      xv[s] = (ok && mvalid) ? *reinterpret_cast<const uint4*>(xrow + k) : make_uint4(0, 0, 0, 0);
+    }
+    if (NORM) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int64_t k = kb + s * 8;
+        float x[8], w[8];
+        unpack8(xv[s], x);
+        if (a.norm_w && k < a.K) {
+          unpack8(*reinterpret_cast<const uint4*>(a.norm_w + k), w);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) w[e] = 1.f;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          ss = fmaf(x[e], x[e], ss);
+          x[e] *= w[e];
+        }
+        xv[s] = make_uint4(pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3]), pack_bf2(x[4], x[5]),
+                           pack_bf2(x[6], x[7]));
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const bf16x8_t bx = as_bf16x8(xv[s]);
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wv[t][s]), bx, acc[t], 0, 0, 0);
+    }
+  }
+
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red[wave][t][j][lane] = acc[t][j];
+  if (NORM) {
+    ss += __shfl_xor(ss, 16, kWave);
+    ss += __shfl_xor(ss, 32, kWave);
+    if (g == 0) ssq[wave][i] = ss;
+  }
+  __syncthreads();
+
+  // Thread tid finalises output (j, l) = (tid / 64, tid % 64) of every tile.
+  const int j = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int64_t mo = m0 + (l & 15);
+  if (mo >= a.M) return;
+  float scale = 1.f;
+  if (NORM) {
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWavesPerBlock; ++w) tot += ssq[w][l & 15];
+    scale = rsqrtf(tot / float(a.K) + a.eps);
+  }
+  float v[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    float sacc = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWavesPerBlock; ++w) sacc += red[w][t][j][l];
+    v[t] = sacc * scale;
+  }
+  const int rofs = 4 * (l >> 4) + j;
+  if (SILU) {
+    const int64_t n = tile0[0] + rofs;
+    if (n < a.N) store_out(a, mo, n, v[0], v[1]);
+  } else {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int64_t n = tile0[t] + rofs;
+      if (n < a.N) store_out(a, mo, n, v[t], 0.f);
+    }
+  }
+}
+
+// Scalar fallback for K % 8 != 0 or unaligned operands: one wave per output
+// row, plain bf16 loads.
+__global__ __launch_bounds__(kBlock) void linear_scalar_kernel(LinearArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t n = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  if (n >= a.N) return;
+  for (int64_t m = 0; m < a.M; ++m) {
+    const uint16_t* x = a.X + m * a.ldx;
+    float acc = 0.f, acc2 = 0.f, ss = 0.f;
+    for (int64_t k = lane; k < a.K; k += kWave) {
+      float xv = bf2f(x[k]);
+      if (a.norm) {
+        ss = fmaf(xv, xv, ss);
+        if (a.norm_w) xv *= bf2f(a.norm_w[k]);
+      }
+      acc = fmaf(bf2f(a.W[n * a.K + k]), xv, acc);
+      if (a.epi == kEpiSilu) acc2 = fmaf(bf2f(a.W2[n * a.K + k]), xv, acc2);
+    }
+    float scale = a.norm ? rsqrtf(wave_sum(ss) / float(a.K) + a.eps) : 1.f;
+    acc = wave_sum(acc) * scale;
+    acc2 = wave_sum(acc2) * scale;
+    if (lane == 0) store_out(a, m, n, acc, acc2);
+  }
+}
+
+template <int M, bool NORM, bool SILU>
+void launch_valu(const LinearArgs& a, hipStream_t s) {
+  constexpr int R = SILU ? 2 : (M == 1 ? 2 : 1);
+  constexpr int U = M <= 2 ? 8 : 4;
+  const int64_t waves = SILU ? a.N : (a.N + R - 1) / R;
+  const int64_t blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
+  hipLaunchKernelGGL((gemv_valu_kernel<M, R, U, NORM, SILU>), dim3(blocks), dim3(kBlock), 0, s, a);
+}
+
+template <bool NORM, bool SILU>
+void launch_valu_m(const LinearArgs& a, hipStream_t s) {
+  switch (a.M) {
+    case 1: launch_valu<1, NORM, SILU>(a, s); break;
+    case 2: launch_valu<2, NORM, SILU>(a, s); break;
+    case 3: launch_valu<3, NORM, SILU>(a, s); break;
+    default: launch_valu<4, NORM, SILU>(a, s); break;
+  }
+}
+
+template <bool NORM, bool SILU>
+void launch_mfma(const LinearArgs& a, hipStream_t s) {
+  constexpr int T = SILU ? 2 : 1;
+  const int64_t blocks = SILU ? (a.N + 15) / 16 : (a.N + 16 * T - 1) / (16 * T);
+  dim3 grid(unsigned(blocks), unsigned((a.M + 15) / 16));
+  hipLaunchKernelGGL((linear_mfma_kernel<T, NORM, SILU>), grid, dim3(kBlock), 0, s, a);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+int launch_linear(const LinearArgs& a, hipStream_t s) {
+  EZ_REQUIRE(a.X && a.W && a.Y, "linear: null pointer");
+  EZ_REQUIRE(a.M >= 1 && a.N >= 1 && a.K >= 1, "linear: sizes must be >= 1 (M=%lld N=%lld K=%lld)",
+             (long long)a.M, (long long)a.N, (long long)a.K);
+  EZ_REQUIRE(a.epi != kEpiSilu || a.W2, "linear: SwiGLU epilogue needs the up-projection weights");
+  EZ_REQUIRE(a.epi != kEpiResid || a.res, "linear: residual epilogue needs the residual");
+  EZ_REQUIRE(a.N < (int64_t(1) << 31) / 16 && a.M < 65536 * 16, "linear: sizes too large");
+  const bool silu = a.epi == kEpiSilu;
+  const bool vec = (a.K % 8 == 0) && (a.ldx % 8 == 0) && aligned16(a.X) && aligned16(a.W) &&
+                   (!silu || aligned16(a.W2)) && (!a.norm_w || aligned16(a.norm_w));
+  if (!vec) {
+    const int64_t blocks = (a.N + kWavesPerBlock - 1) / kWavesPerBlock;
+    hipLaunchKernelGGL(linear_scalar_kernel, dim3(blocks), dim3(kBlock), 0, s, a);
+  } else if (a.M <= 4) {
+    if (a.norm) {
+      silu ? launch_valu_m<true, true>(a, s) : launch_valu_m<true, false>(a, s);
+    } else {
+      silu ? launch_valu_m<false, true>(a, s) : launch_valu_m<false, false>(a, s);
+    }
+  } else {
+    if (a.norm) {
+      silu ? launch_mfma<true, true>(a, s) : launch_mfma<true, false>(a, s);
+    } else {
+      silu ? launch_mfma<false, true>(a, s) : launch_mfma<false, false>(a, s);
+    }
+  }
+  return launch_status("linear");
+}
+
+}  // namespace ez
+
+extern "C" int ezops_gemv_bf16(const void* A, const void* B, void* C, int64_t N, int64_t K,
+                               hipStream_t stream) {
+  ez::LinearArgs a{};
+  a.X = static_cast<const uint16_t*>(A);
+  a.ldx = K;
+  a.W = static_cast<const uint16_t*>(B);
+  a.Y = C;
+  a.ldy = N;
+  a.M = 1;
+  a.N = N;
+  a.K = K;
+  a.epi = ez::kEpiStore;
+  return ez::launch_linear(a, stream);
+}
+
+extern "C" int ezops_linear_bf16(const void* X, int64_t ldx, const void* W, void* Y, int64_t ldy,
+                                 int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  EZ_REQUIRE(ldx >= K && ldy >= N, "linear: leading dimensions too small");
+  ez::LinearArgs a{};
+  a.X = static_cast<const uint16_t*>(X);
+  a.ldx = ldx;
+  a.W = static_cast<const uint16_t*>(W);
+  a.Y = Y;
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.epi = ez::kEpiStore;
+  return ez::launch_linear(a, stream);
+}

@@ -1,0 +1,59 @@
+// Host-side launchers shared between the translation units of libezops_hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ez {
+
+enum Epilogue : int {
+  kEpiStore = 0,   // Y = bf16(acc)
+  kEpiResid = 1,   // Y = bf16(res + bf16(acc))            (o_proj / down_proj + residual)
+  kEpiSilu = 2,    // Y = bf16(bf16(silu(bf16(g))) * bf16(u)), g from W row n, u from W2 row n
+  kEpiStoreF32 = 3 // Y = acc (fp32)
+};
+
+// Y[m, n] = epilogue( sum_k Xn[m, k] * W[n, k] ), m < M, n < N, where
+// Xn = X, or with `norm` set Xn = X * rsqrt(mean(X^2) + eps) * norm_w
+// (the RMSNorm prologue, statistics over the full K row of X).
+struct LinearArgs {
+  const uint16_t* X; int64_t ldx;
+  const uint16_t* W;
+  const uint16_t* W2;          // kEpiSilu: up-projection rows
+  void* Y; int64_t ldy;
+  int64_t M, N, K;
+  const uint16_t* res; int64_t ldr;  // kEpiResid
+  int norm;                    // apply the RMSNorm prologue
+  const uint16_t* norm_w;      // NULL = unit weight
+  float eps;
+  int epi;
+};
+
+int launch_linear(const LinearArgs& a, hipStream_t s);
+
+struct QkRopeArgs {
+  const uint16_t* q; int64_t q_bs;
+  const uint16_t* k; int64_t k_bs;
+  const uint16_t* v; int64_t v_bs;
+  const uint16_t* qw; const uint16_t* kw;
+  const uint16_t* cos; const uint16_t* sin;
+  uint16_t* Kc; uint16_t* Vc;
+  uint16_t* q_out; uint16_t* k_out;
+  int64_t B, H, Hkv, D, S;
+  int64_t position; const int32_t* positions; int64_t pos_offset;
+  float eps;
+};
+int launch_qk_norm_rope(const QkRopeArgs& a, hipStream_t s);
+
+struct AttnArgs {
+  const uint16_t* Q;  // [B, H, D]
+  const uint16_t* K; const uint16_t* V;  // [B, Hkv, S, D]
+  uint16_t* Out;      // [B, H, D]
+  int64_t B, H, Hkv, S, D;
+  const int32_t* kv_lens;
+  float scale;
+};
+size_t attn_workspace_size(int64_t B, int64_t H, int64_t Hkv, int64_t S, int64_t D);
+int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s);
+
+}  // namespace ez

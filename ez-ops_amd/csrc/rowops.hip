@@ -1,0 +1,388 @@
+// Row-wise and whole-tensor fp32/bf16 ops: RMSNorm, softmax, full sum, and
+// the STREAM probes used to measure the HBM peak.
+//
+// Row ops keep the whole row in registers (one HBM read, one write): a block
+// of BS threads holds VPT float4 per thread.  Rows longer than the register
+// budget, or rows that are not 16-byte aligned, take a looped kernel that
+// re-reads the row.
+#include "common.h"
+#include "internal.h"
+#include "status.h"
+#include "../../include/ezops_hip.h"
+
+namespace ez {
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// ---------------------------------------------------------------- RMSNorm f32
+template <int BS, int VPT>
+__global__ __launch_bounds__(BS) void rmsnorm_f32_reg_kernel(const float* __restrict__ X,
+                                                              float* __restrict__ Out,
+                                                              int64_t dim, float eps) {
+  __shared__ float red[BS / kWave];
+  const int64_t row = blockIdx.x;
+  const float4* x = reinterpret_cast<const float4*>(X + row * dim);
+  float4* o = reinterpret_cast<float4*>(Out + row * dim);
+  const int64_t n4 = dim >> 2;
+  float4 v[VPT];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int64_t c = threadIdx.x + int64_t(j) * BS;
+    v[j] = c < n4 ? x[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+  ss = block_reduce<BS / kWave, false>(ss, red);
+  const float r = rsqrtf(ss / float(dim) + eps);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int64_t c = threadIdx.x + int64_t(j) * BS;
+    if (c < n4) o[c] = make_float4(v[j].x * r, v[j].y * r, v[j].z * r, v[j].w * r);
+  }
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_f32_loop_kernel(const float* __restrict__ X,
+                                                               float* __restrict__ Out,
+                                                               int64_t dim, float eps) {
+  __shared__ float red[4];
+  const float* x = X + int64_t(blockIdx.x) * dim;
+  float* o = Out + int64_t(blockIdx.x) * dim;
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < dim; i += 256) ss = fmaf(x[i], x[i], ss);
+  ss = block_reduce<4, false>(ss, red);
+  const float r = rsqrtf(ss / float(dim) + eps);
+  for (int64_t i = threadIdx.x; i < dim; i += 256) o[i] = x[i] * r;
+}
+
+// ------------------------------------------------------ RMSNorm bf16 + weight
+// One block per row; VPT chunks of 8 bf16 per thread.
+template <int BS, int VPT>
+__global__ __launch_bounds__(BS) void rmsnorm_bf16_reg_kernel(const uint16_t* __restrict__ X,
+                                                               const uint16_t* __restrict__ W,
+                                                               uint16_t* __restrict__ Out,
+                                                               int64_t dim, float eps) {
+  __shared__ float red[BS / kWave];
+  const int64_t row = blockIdx.x;
+  const uint4* x = reinterpret_cast<const uint4*>(X + row * dim);
+  const uint4* w = reinterpret_cast<const uint4*>(W);
+  uint4* o = reinterpret_cast<uint4*>(Out + row * dim);
+  const int64_t n8 = dim >> 3;
+  uint4 v[VPT];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int64_t c = threadIdx.x + int64_t(j) * BS;
+    v[j] = c < n8 ? x[c] : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    float f[8];
+    unpack8(v[j], f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
+  }
+  ss = block_reduce<BS / kWave, false>(ss, red);
+  const float r = rsqrtf(ss / float(dim) + eps);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int64_t c = threadIdx.x + int64_t(j) * BS;
+    if (c < n8) {
+      float f[8], g[8];
+      unpack8(v[j], f);
+      if (W) {
+        unpack8(w[c], g);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) g[e] = 1.f;
+      }
+      o[c] = make_uint4(pack_bf2(f[0] * r * g[0], f[1] * r * g[1]), pack_bf2(f[2] * r * g[2], f[3] * r * g[3]),
+                        pack_bf2(f[4] * r * g[4], f[5] * r * g[5]), pack_bf2(f[6] * r * g[6], f[7] * r * g[7]));
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_bf16_loop_kernel(const uint16_t* __restrict__ X,
+                                                                const uint16_t* __restrict__ W,
+                                                                uint16_t* __restrict__ Out,
+                                                                int64_t dim, float eps) {
+  __shared__ float red[4];
+  const uint16_t* x = X + int64_t(blockIdx.x) * dim;
+  uint16_t* o = Out + int64_t(blockIdx.x) * dim;
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < dim; i += 256) {
+    const float f = bf2f(x[i]);
+    ss = fmaf(f, f, ss);
+  }
+  ss = block_reduce<4, false>(ss, red);
+  const float r = rsqrtf(ss / float(dim) + eps);
+  for (int64_t i = threadIdx.x; i < dim; i += 256)
+    o[i] = f2bf(bf2f(x[i]) * r * (W ? bf2f(W[i]) : 1.f));
+}
+
+// ------------------------------------------------------------------ softmax
+template <int BS, int VPT>
+__global__ __launch_bounds__(BS) void softmax_reg_kernel(const float* __restrict__ X,
+                                                          float* __restrict__ Out, int64_t dim) {
+  __shared__ float red[BS / kWave];
+  const int64_t row = blockIdx.x;
+  const float4* x = reinterpret_cast<const float4*>(X + row * dim);
+  float4* o = reinterpret_cast<float4*>(Out + row * dim);
+  const int64_t n4 = dim >> 2;
+  float4 v[VPT];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int64_t c = threadIdx.x + int64_t(j) * BS;
+    v[j] = c < n4 ? x[c] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+  }
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) mx = fmaxf(mx, fmaxf(fmaxf(v[j].x, v[j].y), fmaxf(v[j].z, v[j].w)));
+  mx = block_reduce<BS / kWave, true>(mx, red);
+  const float mb = mx * kLog2e;
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    v[j].x = exp2f(fmaf(v[j].x, kLog2e, -mb));
+    v[j].y = exp2f(fmaf(v[j].y, kLog2e, -mb));
+    v[j].z = exp2f(fmaf(v[j].z, kLog2e, -mb));
+    v[j].w = exp2f(fmaf(v[j].w, kLog2e, -mb));
+    sum += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  }
+  sum = block_reduce<BS / kWave, false>(sum, red);
+  const float inv = 1.0f / sum;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int64_t c = threadIdx.x + int64_t(j) * BS;
+    if (c < n4) o[c] = make_float4(v[j].x * inv, v[j].y * inv, v[j].z * inv, v[j].w * inv);
+  }
+}
+
+__global__ __launch_bounds__(1024) void softmax_loop_kernel(const float* __restrict__ X,
+                                                            float* __restrict__ Out, int64_t dim) {
+  __shared__ float red[16];
+  const float* x = X + int64_t(blockIdx.x) * dim;
+  float* o = Out + int64_t(blockIdx.x) * dim;
+  float mx = -INFINITY;
+  for (int64_t i = threadIdx.x; i < dim; i += 1024) mx = fmaxf(mx, x[i]);
+  mx = block_reduce<16, true>(mx, red);
+  const float mb = mx * kLog2e;
+  float sum = 0.f;
+  for (int64_t i = threadIdx.x; i < dim; i += 1024) sum += exp2f(fmaf(x[i], kLog2e, -mb));
+  sum = block_reduce<16, false>(sum, red);
+  const float inv = 1.0f / sum;
+  for (int64_t i = threadIdx.x; i < dim; i += 1024) o[i] = exp2f(fmaf(x[i], kLog2e, -mb)) * inv;
+}
+
+// --------------------------------------------------------------- full sum
+// Stage 1: block b sums a fixed, strided share of the float4s into
+// partial[b]; the last block to finish sums partial[0..G) in index order.
+// The grid size depends only on n, so the result is bitwise reproducible.
+constexpr int kSumBlock = 256;
+constexpr int kSumUnroll = 8;
+constexpr int kSumMaxBlocks = 1024;
+
+int64_t sum_blocks(int64_t n) {
+  const int64_t per_block = int64_t(kSumBlock) * 4 * kSumUnroll;
+  int64_t g = (n + per_block - 1) / per_block;
+  if (g < 1) g = 1;
+  return g > kSumMaxBlocks ? kSumMaxBlocks : g;
+}
+
+__global__ __launch_bounds__(kSumBlock) void sum_kernel(const float* __restrict__ A, int64_t n,
+                                                        bool vec, float* __restrict__ partial,
+                                                        int* counter, float* __restrict__ Out) {
+  __shared__ float red[kSumBlock / kWave];
+  const int64_t G = gridDim.x;
+  const int64_t stride = G * kSumBlock;
+  float acc[kSumUnroll];
+#pragma unroll
+  for (int u = 0; u < kSumUnroll; ++u) acc[u] = 0.f;
+  int64_t tail_start = 0;
+  if (vec) {
+    const float4* a4 = reinterpret_cast<const float4*>(A);
+    const int64_t n4 = n >> 2;
+    int64_t i = int64_t(blockIdx.x) * kSumBlock + threadIdx.x;
+    for (; i + (kSumUnroll - 1) * stride < n4; i += kSumUnroll * stride) {
+      float4 v[kSumUnroll];
+#pragma unroll
+      for (int u = 0; u < kSumUnroll; ++u) v[u] = a4[i + u * stride];
+#pragma unroll
+      for (int u = 0; u < kSumUnroll; ++u) acc[u] += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+    }
+    for (; i < n4; i += stride) {
+      const float4 v = a4[i];
+      acc[0] += (v.x + v.y) + (v.z + v.w);
+    }
+    tail_start = n4 << 2;
+  }
+  // scalar remainder (all of it when A is not 16-byte aligned)
+  for (int64_t i = tail_start + int64_t(blockIdx.x) * kSumBlock + threadIdx.x; i < n; i += stride)
+    acc[1] += A[i];
+  float s = 0.f;
+#pragma unroll
+  for (int u = 0; u < kSumUnroll; ++u) s += acc[u];
+  s = block_reduce<kSumBlock / kWave, false>(s, red);
+  if (threadIdx.x == 0) partial[blockIdx.x] = s;
+  if (!arrive_last(counter, int(G))) return;
+  float t = 0.f;
+  for (int64_t i = threadIdx.x; i < G; i += kSumBlock) t += __builtin_nontemporal_load(partial + i);
+  t = block_reduce<kSumBlock / kWave, false>(t, red);
+  if (threadIdx.x == 0) Out[0] = t;
+}
+
+// ------------------------------------------------------------ HBM probes
+__global__ __launch_bounds__(256) void probe_kernel(int kind, float4* __restrict__ a,
+                                                    const float4* __restrict__ b,
+                                                    const float4* __restrict__ c, int64_t n4, float s) {
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (kind == 0) {
+    float acc = 0.f;
+    for (; i < n4; i += stride) {
+      const float4 v = b[i];
+      acc += (v.x + v.y) + (v.z + v.w);
+    }
+    if (acc == 1234.5f) a[0].x = acc;  // keeps the loads alive; practically never stores
+  } else if (kind == 1) {
+    for (; i < n4; i += stride) a[i] = make_float4(s, s, s, s);
+  } else if (kind == 2) {
+    for (; i < n4; i += stride) a[i] = b[i];
+  } else {
+    for (; i < n4; i += stride) {
+      const float4 x = b[i], y = c[i];
+      a[i] = make_float4(fmaf(s, y.x, x.x), fmaf(s, y.y, x.y), fmaf(s, y.z, x.z), fmaf(s, y.w, x.w));
+    }
+  }
+}
+
+int num_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+  }
+  return cus;
+}
+
+template <int BS>
+void launch_rms_f32(const float* X, float* O, int64_t rows, int64_t dim, float eps, hipStream_t s) {
+  const int64_t vpt = (dim / 4 + BS - 1) / BS;
+  const dim3 g{unsigned(rows), 1, 1}, b{unsigned(BS), 1, 1};
+  if (vpt <= 1) hipLaunchKernelGGL((rmsnorm_f32_reg_kernel<BS, 1>), g, b, 0, s, X, O, dim, eps);
+  else if (vpt <= 2) hipLaunchKernelGGL((rmsnorm_f32_reg_kernel<BS, 2>), g, b, 0, s, X, O, dim, eps);
+  else if (vpt <= 4) hipLaunchKernelGGL((rmsnorm_f32_reg_kernel<BS, 4>), g, b, 0, s, X, O, dim, eps);
+  else hipLaunchKernelGGL((rmsnorm_f32_reg_kernel<BS, 8>), g, b, 0, s, X, O, dim, eps);
+}
+
+template <int BS>
+void launch_rms_bf16(const uint16_t* X, const uint16_t* W, uint16_t* O, int64_t rows, int64_t dim,
+                     float eps, hipStream_t s) {
+  const int64_t vpt = (dim / 8 + BS - 1) / BS;
+  const dim3 g{unsigned(rows), 1, 1}, b{unsigned(BS), 1, 1};
+  if (vpt <= 1) hipLaunchKernelGGL((rmsnorm_bf16_reg_kernel<BS, 1>), g, b, 0, s, X, W, O, dim, eps);
+  else if (vpt <= 2) hipLaunchKernelGGL((rmsnorm_bf16_reg_kernel<BS, 2>), g, b, 0, s, X, W, O, dim, eps);
+  else if (vpt <= 4) hipLaunchKernelGGL((rmsnorm_bf16_reg_kernel<BS, 4>), g, b, 0, s, X, W, O, dim, eps);
+  else hipLaunchKernelGGL((rmsnorm_bf16_reg_kernel<BS, 8>), g, b, 0, s, X, W, O, dim, eps);
+}
+
+template <int BS>
+void launch_softmax(const float* X, float* O, int64_t rows, int64_t dim, hipStream_t s) {
+  const int64_t vpt = (dim / 4 + BS - 1) / BS;
+  const dim3 g{unsigned(rows), 1, 1}, b{unsigned(BS), 1, 1};
+  if (vpt <= 1) hipLaunchKernelGGL((softmax_reg_kernel<BS, 1>), g, b, 0, s, X, O, dim);
+  else if (vpt <= 2) hipLaunchKernelGGL((softmax_reg_kernel<BS, 2>), g, b, 0, s, X, O, dim);
+  else if (vpt <= 4) hipLaunchKernelGGL((softmax_reg_kernel<BS, 4>), g, b, 0, s, X, O, dim);
+  else hipLaunchKernelGGL((softmax_reg_kernel<BS, 8>), g, b, 0, s, X, O, dim);
+}
+
+}  // namespace
+}  // namespace ez
+
+using namespace ez;
+
+extern "C" int ezops_rmsnorm_f32(const float* X, float* Out, int64_t rows, int64_t dim, float eps,
+                                 hipStream_t s) {
+  EZ_REQUIRE(X && Out, "rmsnorm_f32: null pointer");
+  EZ_REQUIRE(rows >= 1 && dim >= 1 && rows < (int64_t(1) << 31), "rmsnorm_f32: bad shape");
+  const bool vec = dim % 4 == 0 && aligned16(X) && aligned16(Out);
+  if (!vec || dim > 32768) {
+    hipLaunchKernelGGL(rmsnorm_f32_loop_kernel, dim3(unsigned(rows)), dim3(256), 0, s, X, Out, dim, eps);
+  } else if (dim <= 2048) {
+    launch_rms_f32<64>(X, Out, rows, dim, eps, s);
+  } else if (dim <= 8192) {
+    launch_rms_f32<256>(X, Out, rows, dim, eps, s);
+  } else {
+    launch_rms_f32<1024>(X, Out, rows, dim, eps, s);
+  }
+  return launch_status("rmsnorm_f32");
+}
+
+extern "C" int ezops_rmsnorm_bf16(const void* Xv, const void* Wv, void* Ov, int64_t rows, int64_t dim,
+                                  float eps, hipStream_t s) {
+  auto X = static_cast<const uint16_t*>(Xv);
+  auto W = static_cast<const uint16_t*>(Wv);
+  auto O = static_cast<uint16_t*>(Ov);
+  EZ_REQUIRE(X && O, "rmsnorm_bf16: null pointer");
+  EZ_REQUIRE(rows >= 1 && dim >= 1 && rows < (int64_t(1) << 31), "rmsnorm_bf16: bad shape");
+  const bool vec = dim % 8 == 0 && aligned16(X) && aligned16(O) && (!W || aligned16(W));
+  if (!vec || dim > 65536) {
+    hipLaunchKernelGGL(rmsnorm_bf16_loop_kernel, dim3(unsigned(rows)), dim3(256), 0, s, X, W, O, dim, eps);
+  } else if (dim <= 4096) {
+    launch_rms_bf16<64>(X, W, O, rows, dim, eps, s);
+  } else if (dim <= 16384) {
+    launch_rms_bf16<256>(X, W, O, rows, dim, eps, s);
+  } else {
+    launch_rms_bf16<1024>(X, W, O, rows, dim, eps, s);
+  }
+  return launch_status("rmsnorm_bf16");
+}
+
+extern "C" int ezops_softmax_f32(const float* X, float* Out, int64_t rows, int64_t dim, hipStream_t s) {
+  EZ_REQUIRE(X && Out, "softmax_f32: null pointer");
+  EZ_REQUIRE(rows >= 1 && dim >= 1 && rows < (int64_t(1) << 31), "softmax_f32: bad shape");
+  const bool vec = dim % 4 == 0 && aligned16(X) && aligned16(Out);
+  if (!vec || dim > 32768) {
+    hipLaunchKernelGGL(softmax_loop_kernel, dim3(unsigned(rows)), dim3(1024), 0, s, X, Out, dim);
+  } else if (dim <= 2048) {
+    launch_softmax<64>(X, Out, rows, dim, s);
+  } else if (dim <= 8192) {
+    launch_softmax<256>(X, Out, rows, dim, s);
+  } else {
+    launch_softmax<1024>(X, Out, rows, dim, s);
+  }
+  return launch_status("softmax_f32");
+}
+
+extern "C" size_t ezops_reduce_sum_workspace_size(int64_t n) {
+  // partial sums + one arrival counter, 256-byte aligned
+  return size_t(((sum_blocks(n) * 4 + 255) / 256) * 256 + 256);
+}
+
+extern "C" int ezops_reduce_sum_f32(const float* A, float* Out, int64_t n, void* ws, size_t ws_bytes,
+                                    hipStream_t s) {
+  EZ_REQUIRE(A && Out && ws, "reduce_sum_f32: null pointer");
+  EZ_REQUIRE(n >= 1, "reduce_sum_f32: n must be >= 1");
+  EZ_REQUIRE(ws_bytes >= ezops_reduce_sum_workspace_size(n), "reduce_sum_f32: workspace too small");
+  const int64_t G = sum_blocks(n);
+  float* partial = static_cast<float*>(ws);
+  int* counter = reinterpret_cast<int*>(static_cast<char*>(ws) + ((G * 4 + 255) / 256) * 256);
+  hipLaunchKernelGGL(sum_kernel, dim3(unsigned(G)), dim3(kSumBlock), 0, s, A, n, aligned16(A), partial,
+                     counter, Out);
+  return launch_status("reduce_sum_f32");
+}
+
+extern "C" int ezops_hbm_probe(int kind, float* a, const float* b, const float* c, int64_t n, float sc,
+                               hipStream_t s) {
+  EZ_REQUIRE(kind >= 0 && kind <= 3, "hbm_probe: kind must be 0..3");
+  EZ_REQUIRE(a && (kind == 1 || b) && (kind != 3 || c), "hbm_probe: null pointer");
+  EZ_REQUIRE(n >= 4 && n % 4 == 0, "hbm_probe: n must be a positive multiple of 4");
+  const int64_t blocks = int64_t(num_cus()) * 8;
+  hipLaunchKernelGGL(probe_kernel, dim3(unsigned(blocks)), dim3(256), 0, s, kind, reinterpret_cast<float4*>(a),
+                     reinterpret_cast<const float4*>(b), reinterpret_cast<const float4*>(c), n / 4, sc);
+  return launch_status("hbm_probe");
+}

@@ -1,0 +1,168 @@
+/*
+ * ezops_hip.h - C ABI of libezops_hip.so, the MI355X (gfx950) operator
+ * backend for the ez-ops decode hot path.
+ *
+ * Conventions shared by every entry point:
+ *   - Tensors are raw device pointers to contiguous row-major memory.  bf16
+ *     tensors are passed as `void*` (2-byte elements), fp32 as `float*`.
+ *   - Sizes are int64_t element counts.
+ *   - Work is enqueued on `stream`; nothing synchronises, allocates or reads
+ *     device memory back, so every call can be captured into a HIP graph.
+ *   - Scratch memory is caller-owned: `*_workspace_size` gives the byte count
+ *     and the caller passes a zero-filled buffer of at least that size once;
+ *     the kernels leave their counters at zero again after every call, so
+ *     the same workspace serves later calls on the same stream.  Calls that
+ *     overlap in time must not share a workspace.
+ *   - Return value: 0 on success, EZOPS_EINVAL (-22) for rejected arguments,
+ *     or the hipError_t of a failed launch; ezops_hip_last_error() describes
+ *     the last failure of the calling thread.
+ *
+ * Each entry point names the reference (coffee0224/ez-ops) interface it
+ * replaces as a drop-in behind the reference's op/registry API.
+ */
+#ifndef EZOPS_HIP_H
+#define EZOPS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EZOPS_HIP_ABI_VERSION 1
+#define EZOPS_EINVAL (-22)
+
+int ezops_hip_abi_version(void);
+const char* ezops_hip_last_error(void);
+
+/* bf16 GEMV: C[n] = sum_k A[k] * B[n, k], fp32 accumulation, one bf16 rounding.
+ * A [K], B [N, K], C [N].  Any N >= 1, K >= 1.
+ * Replaces: gemv_cu(A, B, C) (ezops/kernels/gemv/gemv_cu.cu:71-87), reached
+ * through GemvOp.forward (ezops/ops/gemv.py:25-26). */
+int ezops_gemv_bf16(const void* A, const void* B, void* C, int64_t N, int64_t K,
+                    hipStream_t stream);
+
+/* Skinny bf16 linear layer: Y[m, n] = sum_k X[m, k] * W[n, k] for m < M.
+ * X [M, K] (row stride ldx), W [N, K], Y [M, N] (row stride ldy); M >= 1.
+ * Rows are processed 16 at a time with MFMA when M > 4.
+ * Replaces: the `x @ W.T` projections inside the fused decode kernels
+ * (ezops/kernels/fused_o_proj_ffn/fused_o_proj_ffn_triton.py:31-231,
+ * ezops/kernels/qwen3_dense_decode/qwen3_dense_decode_triton.py:37-271). */
+int ezops_linear_bf16(const void* X, int64_t ldx, const void* W, void* Y, int64_t ldy,
+                      int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
+/* fp32 RMSNorm without weight: Out = X * rsqrt(mean(X^2) + eps), per row.
+ * X, Out [rows, dim].
+ * Replaces: rmsnorm_kernel host launch (ezops/kernels/rmsnorm/rmsnorm_cu.cu:51-63)
+ * behind RmsNormOp (ezops/ops/rmsnorm.py:7-36). */
+int ezops_rmsnorm_f32(const float* X, float* Out, int64_t rows, int64_t dim, float eps,
+                      hipStream_t stream);
+
+/* bf16 Qwen3 RMSNorm with weight: Out = bf16(x * rsqrt(mean(x^2) + eps) * w),
+ * fp32 statistics.  X, Out [rows, dim]; W [dim] (NULL = unit weight).
+ * Replaces: FusedOProjFfnOp._rmsnorm / Qwen3DenseDecodeOp._rmsnorm
+ * (ezops/ops/fused_o_proj_ffn.py:107-110, ezops/ops/qwen3_dense_decode.py:137-140). */
+int ezops_rmsnorm_bf16(const void* X, const void* W, void* Out, int64_t rows, int64_t dim,
+                       float eps, hipStream_t stream);
+
+/* fp32 row softmax over the last dim; X, Out [rows, dim].
+ * Replaces: softmax_kernel host launch (ezops/kernels/softmax/softmax_cu.cu:78-89)
+ * behind SoftmaxOp (ezops/ops/softmax.py:7-34). */
+int ezops_softmax_f32(const float* X, float* Out, int64_t rows, int64_t dim, hipStream_t stream);
+
+/* Deterministic fp32 full sum: Out[0] = sum(A[0:n]).
+ * Replaces: reduce_cu (ezops/kernels/reduce/reduce_cu.cu:233-282) behind
+ * ReduceOp (ezops/ops/reduce.py:7-31).  Two-stage, fixed order, no float atomics. */
+size_t ezops_reduce_sum_workspace_size(int64_t n);
+int ezops_reduce_sum_f32(const float* A, float* Out, int64_t n, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream);
+
+/* Split-KV GQA decode attention, one query token per sequence.
+ * Q [B, H, D] (== [B, H, 1, D]), K/V [B, Hkv, S, D], Out [B, H, D]; bf16.
+ * H % Hkv == 0, H / Hkv <= 16, D in {64, 128}.  kv_lens [B] int32 (NULL = S
+ * for every sequence) limits sequence b to slots [0, kv_lens[b]).
+ * scale <= 0 selects 1/sqrt(D).
+ * Replaces: flash_decode_tilelang_gqa_split (+ combine)
+ * (ezops/kernels/attn_decode/attn_decode_tl.py:316-470, 617-627) and
+ * attn_decode_cu (ezops/kernels/attn_decode/attn_decode_cu.cu:140-181)
+ * behind AttnDecodeOp (ezops/ops/attn_decode.py:9-67). */
+size_t ezops_attn_decode_workspace_size(int64_t B, int64_t H, int64_t Hkv, int64_t S, int64_t D);
+int ezops_attn_decode_bf16(const void* Q, const void* K, const void* V, void* Out, int64_t B,
+                           int64_t H, int64_t Hkv, int64_t S, int64_t D, const int32_t* kv_lens,
+                           float scale, void* workspace, size_t workspace_bytes,
+                           hipStream_t stream);
+
+/* Qwen3 per-head QK RMSNorm + half-split RoPE + KV-cache write, one decode step.
+ * q [B, H, D] (batch stride q_bstride elements), k/v [B, Hkv, D] (strides
+ * k_bstride / v_bstride), q_norm_w / k_norm_w [D] (NULL = unit), cos/sin
+ * [S, D] HF tables (both NULL = no RoPE), caches [B, Hkv, S, D].
+ * Position of sequence b: (positions ? positions[b] : position) + pos_offset.
+ * Writes q_out [B, H, D], k_out [B, Hkv, D] (k_out may be NULL) and the cache slot.
+ * Replaces: FusedQkNormRopeOp backends (ezops/kernels/fused_qk_norm_rope/
+ * fused_qk_norm_rope_triton.py:23-190, fused_qk_norm_rope_tl.py:32-165). */
+int ezops_qk_norm_rope_bf16(const void* q, int64_t q_bstride, const void* k, int64_t k_bstride,
+                            const void* v, int64_t v_bstride, const void* q_norm_w,
+                            const void* k_norm_w, const void* cos, const void* sin,
+                            void* K_cache, void* V_cache, void* q_out, void* k_out, int64_t B,
+                            int64_t H, int64_t Hkv, int64_t D, int64_t S, int64_t position,
+                            const int32_t* positions, int64_t pos_offset, float eps,
+                            hipStream_t stream);
+
+/* Fused o_proj + post-norm + SwiGLU FFN (batch x 1 token), bf16:
+ *   x2 = residual + attn @ Wo^T ; xn = rmsnorm(x2) * post_norm_w
+ *   out = x2 + (silu(xn @ Wg^T) * (xn @ Wu^T)) @ Wd^T
+ * attn [B, QR], residual/out [B, HS], Wo [HS, QR], post_norm_w [HS],
+ * Wg/Wu [IS, HS], Wd [HS, IS].  Wu may equal Wg + IS*HS (fused [gate|up]).
+ * Replaces: FusedOProjFfnOp backends (ezops/kernels/fused_o_proj_ffn/
+ * fused_o_proj_ffn_persistent_tl.py:56-286, fused_o_proj_ffn_triton.py:31-231). */
+size_t ezops_o_proj_ffn_workspace_size(int64_t B, int64_t HS, int64_t IS, int64_t QR);
+int ezops_o_proj_ffn_bf16(const void* attn, const void* residual, const void* Wo,
+                          const void* post_norm_w, const void* Wg, const void* Wu, const void* Wd,
+                          void* out, int64_t B, int64_t HS, int64_t IS, int64_t QR, float eps,
+                          void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* One Qwen3 dense decoder-layer decode step (see ezops/ops/qwen3_dense_decode.py).
+ * Replaces: Qwen3DenseDecodeOp backends (ezops/kernels/qwen3_dense_decode/
+ * qwen3_dense_decode_triton.py:273-384, qwen3_dense_decode_persistent_tl.py:566-609). */
+typedef struct ezops_qwen3_layer {
+  /* shapes */
+  int64_t B, S, HS, IS, H, Hkv, D;
+  float eps;
+  /* inputs (bf16 unless noted) */
+  const void* hidden;       /* [B, HS] */
+  void* K_cache;            /* [B, Hkv, S, D], slot kv_len-1 written */
+  void* V_cache;            /* [B, Hkv, S, D], slot kv_len-1 written */
+  const void* Wqkv;         /* [H*D + 2*Hkv*D, HS], rows [q | k | v] */
+  const void* Wo;           /* [HS, H*D] */
+  const void* Wgu;          /* [2*IS, HS], rows [gate | up] */
+  const void* Wd;           /* [HS, IS] */
+  const void* in_norm_w;    /* [HS] or NULL (unit) */
+  const void* q_norm_w;     /* [D] or NULL */
+  const void* k_norm_w;     /* [D] or NULL */
+  const void* post_norm_w;  /* [HS] or NULL */
+  const void* cos;          /* [S, D] or NULL (no RoPE) */
+  const void* sin;          /* [S, D] or NULL */
+  const int32_t* kv_lens;   /* [B] int32 or NULL (= S for every sequence) */
+  /* output */
+  void* out;                /* [B, HS] */
+} ezops_qwen3_layer;
+
+size_t ezops_qwen3_layer_workspace_size(const ezops_qwen3_layer* p);
+int ezops_qwen3_dense_decode_bf16(const ezops_qwen3_layer* p, void* workspace,
+                                  size_t workspace_bytes, hipStream_t stream);
+
+/* STREAM-style HBM probes used to measure the chip's bandwidth peak
+ * (replaces benchmarks/hardware/memory/hbm_saturation.cu:49-90):
+ * kind 0 = read (sum into out[0..]), 1 = write, 2 = copy, 3 = triad
+ * a = b + s*c.  n = float count per array. */
+int ezops_hbm_probe(int kind, float* a, const float* b, const float* c, int64_t n, float s,
+                    hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EZOPS_HIP_H */

@@ -1,0 +1,54 @@
+"""The C-ABI library loads and exports every entry point of include/ezops_hip.h (CPU only).
+
+Only argument-validation paths are exercised here: they return before any
+HIP call, so no GPU is needed.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from ezops import _hip
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "ezops_hip.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(ezops_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _hip.lib()
+    names = declared_functions()
+    assert len(names) >= 17
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_hip.SIGNATURES), "ctypes table and header disagree"
+    assert lib.ezops_hip_abi_version() == _hip.ABI_VERSION
+
+
+def test_struct_layout_matches_header():
+    # int64 x7, float (+pad), then 15 pointers
+    assert ctypes.sizeof(_hip.Qwen3LayerParams) == 7 * 8 + 8 + 15 * 8
+
+
+def test_invalid_arguments_return_einval():
+    lib = _hip.lib()
+    assert lib.ezops_gemv_bf16(None, None, None, 16, 16, None) == _hip.EINVAL
+    assert b"null" in lib.ezops_hip_last_error()
+    assert lib.ezops_softmax_f32(None, None, 4, 4, None) == _hip.EINVAL
+    assert lib.ezops_hbm_probe(9, None, None, None, 16, 1.0, None) == _hip.EINVAL
+    with pytest.raises(RuntimeError, match="null"):
+        _hip.call("ezops_rmsnorm_f32", None, None, 1, 1, 1e-6, None)
+
+
+def test_workspace_sizes():
+    lib = _hip.lib()
+    assert lib.ezops_reduce_sum_workspace_size(1 << 28) >= 4 * 1024
+    assert lib.ezops_attn_decode_workspace_size(32, 32, 8, 8192, 128) > 0
+    assert lib.ezops_attn_decode_workspace_size(0, 32, 8, 8192, 128) == 0
+    p = _hip.Qwen3LayerParams(B=1, S=16384, HS=4096, IS=12288, H=32, Hkv=8, D=128)
+    assert lib.ezops_qwen3_layer_workspace_size(ctypes.byref(p)) > 12288 * 2

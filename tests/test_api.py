@@ -1,0 +1,140 @@
+"""Host-side API: registry, op validation, roofline counts, torch ``ref`` ops vs oracle (CPU)."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from ezops import (AttnDecodeOp, FusedOProjFfnOp, FusedQkNormRopeOp, GemvOp, Qwen3DenseDecodeOp, ReduceOp,
+                   RmsNormOp, SoftmaxOp, get_kernel, list_backends, list_ops, register_kernel)
+from ezops.ops.utils.accuracy import bitwise_equal, sqnr_db
+from ezops.ops.utils.roofline import RooflineResult, measure_roofline
+
+OPS = ["attn_decode", "fused_o_proj_ffn", "fused_qk_norm_rope", "gemv", "qwen3_dense_decode", "reduce",
+       "rmsnorm", "softmax"]
+
+
+def n(x):
+    return x.float().numpy()
+
+
+def test_registry_single_hip_backend():
+    assert list_ops() == OPS
+    for op in OPS:
+        assert list_backends(op) == ["hip"]
+        cls = get_kernel(op, "hip")
+        assert cls.op_name == op and cls.backend == "hip"
+
+
+def test_registry_errors():
+    with pytest.raises(KeyError, match="Available backends for 'gemv': \\['hip'\\]"):
+        get_kernel("gemv", "triton")
+    with pytest.raises(ValueError, match="already registered"):
+        register_kernel("gemv", "hip")(type("Dup", (), {}))
+
+
+def test_validation_errors():
+    with pytest.raises(ValueError, match="power of two"):
+        FusedQkNormRopeOp(1, num_heads=16, head_dim=100, max_seq_len=128, position=0)
+    with pytest.raises(ValueError, match="position"):
+        FusedQkNormRopeOp(1, num_heads=16, head_dim=128, max_seq_len=128, position=128)
+    with pytest.raises(ValueError, match="divisible"):
+        FusedQkNormRopeOp(1, num_heads=16, head_dim=128, max_seq_len=128, position=0, num_kv_heads=6)
+    with pytest.raises(ValueError, match="divisible"):
+        Qwen3DenseDecodeOp(1, 128, num_heads=16, head_dim=128, hidden_size=2048, intermediate_size=6144,
+                           num_kv_heads=6)
+    with pytest.raises(ValueError, match="divisible"):
+        AttnDecodeOp(1, 16, 128, 128, num_kv_heads=6)
+    # tile divisibility is enforced by the backend kernel (reference test targets its own backend)
+    with pytest.raises(ValueError, match="divisible"):
+        FusedOProjFfnOp(1, hidden_size=2048, intermediate_size=6200, num_heads=16, head_dim=128, backend="hip")
+    with pytest.raises(ValueError, match="seq_len"):
+        Qwen3DenseDecodeOp(1, 0, 2048, 6144, 16, 128)
+    with pytest.raises(ValueError, match="kv_lens"):
+        Qwen3DenseDecodeOp(1, 16, 256, 512, 4, 64, kv_lens=[17])
+    with pytest.raises(ValueError, match="head_dim"):
+        AttnDecodeOp(1, 4, 16, 96, backend="hip")
+
+
+def test_roofline_known_answers():
+    a, b = torch.randn(32, 64), torch.randn(64, 128)
+    r = measure_roofline(lambda x, y: x @ y, (a, b), {})
+    assert r.flops == 2 * 32 * 64 * 128 and r.bytes == a.nbytes + b.nbytes + 32 * 128 * 4
+    x = torch.randn(1024)
+    r = measure_roofline(lambda u, v: u + v, (x, x), {})
+    assert r.flops == 1024 and r.bytes == 3 * 4096
+    assert RooflineResult(10, 0, 0).arithmetic_intensity == float("inf")
+    # decode-path byte counts of the benchmark configs
+    assert GemvOp(4096, 4096).get_roofline().bytes == 33_570_816
+    assert AttnDecodeOp(32, 32, 8192, 128, num_kv_heads=8).get_roofline().bytes == 1_074_266_112
+    assert SoftmaxOp(4096, 32768).get_roofline().bytes == 1_073_741_824
+    assert ReduceOp(1 << 28).get_roofline().bytes == 1_073_741_828
+
+
+def test_accuracy_helpers():
+    a = torch.tensor([0.0, 1.0])
+    assert bitwise_equal(a, a.clone()) and not bitwise_equal(a, torch.tensor([-0.0, 1.0]))
+    assert sqnr_db(a, a) == float("inf")
+
+
+# --- torch ``ref`` backend (the reference's _ref_forward semantics) vs the numpy oracle
+
+def test_ref_gemv_rms_softmax_reduce():
+    torch.manual_seed(0)
+    op = GemvOp(64, 96)
+    A, B, C = op.gen_data("cpu")
+    op(A, B, C)
+    np.testing.assert_allclose(n(C), oracle.gemv(n(A), n(B).T.copy()), rtol=1e-2, atol=1e-2)
+    op = RmsNormOp(5, 100)
+    X, O = op.gen_data("cpu")
+    op(X, O)
+    np.testing.assert_allclose(n(O), oracle.rmsnorm_f32(n(X)), rtol=1e-5, atol=1e-6)
+    op = RmsNormOp(4, 256, dtype=torch.bfloat16, weighted=True)
+    X, W, O = op.gen_data("cpu")
+    op(X, W, O)
+    np.testing.assert_allclose(n(O), oracle.rmsnorm_bf16(n(X), n(W)), rtol=1e-2, atol=2e-2)
+    op = SoftmaxOp(3, 1000)
+    X, O = op.gen_data("cpu")
+    op(X, O)
+    np.testing.assert_allclose(n(O), oracle.softmax(n(X)), rtol=1e-5, atol=1e-6)
+    op = ReduceOp(10001)
+    A, O = op.gen_data("cpu")
+    op(A, O)
+    assert op.check(O, torch.from_numpy(oracle.reduce_sum(n(A))))
+
+
+def test_ref_attn_and_qk_rope():
+    torch.manual_seed(1)
+    op = AttnDecodeOp(2, 8, 40, 64, num_kv_heads=2)
+    Q, K, V = op.gen_data("cpu")
+    lens = torch.tensor([40, 17], dtype=torch.int32)
+    out = op(Q, K, V, lens)
+    ref = oracle.attn_decode(n(Q)[:, :, 0], n(K), n(V), lens.numpy())
+    np.testing.assert_allclose(n(out)[:, :, 0], ref, rtol=1e-2, atol=1e-2)
+    op = FusedQkNormRopeOp(2, 8, 64, 50, position=[3, 49], num_kv_heads=2)
+    data = op.gen_data("cpu")
+    npy = [n(x) for x in data]
+    qo, ko = op(*data)
+    q2, k2, Kc, Vc = oracle.qk_norm_rope(*npy, positions=[3, 49])
+    np.testing.assert_allclose(n(qo), q2, rtol=1e-2, atol=1e-2)
+    np.testing.assert_allclose(n(ko), k2, rtol=1e-2, atol=1e-2)
+    np.testing.assert_array_equal(n(data[8]), Vc)
+
+
+def test_ref_fused_and_layer():
+    torch.manual_seed(2)
+    op = FusedOProjFfnOp(2, 128, 192, 4, 32)
+    data = op.gen_data("cpu")
+    out = op(*data)
+    ref = oracle.o_proj_ffn(*[n(x) for x in data])
+    assert op.check(out, torch.from_numpy(ref))
+    op = Qwen3DenseDecodeOp(2, 24, 128, 192, 4, 32, num_kv_heads=2, kv_lens=[24, 9], norm_weights=True,
+                            rope_theta=1e6)
+    data = op.gen_data("cpu")
+    npy = [n(x) for x in data]
+    out = op(*data)
+    ref, Kc, Vc = oracle.qwen3_layer(*npy[:7], 4, 2, 32, kv_lens=[24, 9], in_norm_w=npy[7], q_norm_w=npy[8],
+                                     k_norm_w=npy[9], post_norm_w=npy[10], cos=npy[11], sin=npy[12])
+    assert op.check(out, torch.from_numpy(ref))
+    np.testing.assert_allclose(n(data[1]), Kc, rtol=1e-2, atol=1e-2)
+    np.testing.assert_array_equal(n(data[2]), Vc)

@@ -1,0 +1,102 @@
+"""Fused decode ops on HIP vs the numpy oracle (GPU).
+
+Mirrors the reference's parity tests (tests/test_fused_qk_norm_rope.py:10-64,
+tests/test_fused_o_proj_ffn.py:14-40, tests/test_qwen3_dense_decode.py:17-64)
+with the oracle as the checker, plus the Qwen3-8B benchmark shapes.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from ezops import FusedOProjFfnOp, FusedQkNormRopeOp, Qwen3DenseDecodeOp, list_backends
+
+pytestmark = pytest.mark.gpu
+BF_TOL = dict(rtol=1e-2, atol=2e-2)
+
+QWEN3_VL_2B_HEADS = dict(num_heads=16, head_dim=128, num_kv_heads=8)
+QWEN3_VL_2B = dict(hidden_size=2048, intermediate_size=6144, num_heads=16, head_dim=128)
+QWEN3_0_6B = dict(hidden_size=1024, intermediate_size=3072, num_heads=16, head_dim=128)
+QWEN3_8B = dict(hidden_size=4096, intermediate_size=12288, num_heads=32, head_dim=128)
+
+
+def n(x):
+    return x.detach().float().cpu().numpy()
+
+
+@pytest.mark.parametrize("batch,max_seq_len,position,num_kv_heads", [
+    (1, 128, 0, 8), (1, 1024, 512, 8), (2, 1025, 1024, 8), (1, 4096, 1, 4), (1, 100, 50, 16), (1, 33, 17, 2),
+    (4, 2048, [5, 2047, 0, 1000], 8),  # one position per sequence
+])
+def test_fused_qk_norm_rope(batch, max_seq_len, position, num_kv_heads):
+    assert list_backends("fused_qk_norm_rope") == ["hip"]
+    kw = {**QWEN3_VL_2B_HEADS, "num_kv_heads": num_kv_heads}
+    torch.manual_seed(42)
+    op = FusedQkNormRopeOp(batch, max_seq_len=max_seq_len, position=position, backend="hip", **kw)
+    data = op.gen_data()
+    K0, V0 = data[7].clone(), data[8].clone()
+    q_out, k_out = op(*data)
+    pos = np.broadcast_to(np.asarray(position), (batch,))
+    rq, rk, rK, rV = oracle.qk_norm_rope(*[n(x) for x in data[:7]], n(K0), n(V0), pos)
+    np.testing.assert_allclose(n(q_out), rq, **BF_TOL)
+    np.testing.assert_allclose(n(k_out), rk, **BF_TOL)
+    Kc, Vc = data[7], data[8]
+    for b in range(batch):
+        p = int(pos[b])
+        np.testing.assert_allclose(n(Kc[b, :, p]), rk[b], **BF_TOL)
+        assert torch.equal(Vc[b, :, p], data[2][b])
+        mask = torch.ones(max_seq_len, dtype=torch.bool, device=Kc.device)
+        mask[p] = False
+        assert torch.equal(Kc[b][:, mask], K0[b][:, mask])
+        assert torch.equal(Vc[b][:, mask], V0[b][:, mask])
+
+
+@pytest.mark.parametrize("batch,shape", [(1, QWEN3_VL_2B), (1, QWEN3_0_6B), (2, QWEN3_VL_2B), (4, QWEN3_VL_2B),
+                                         (1, QWEN3_8B), (16, QWEN3_8B), (7, QWEN3_0_6B)])
+def test_fused_o_proj_ffn(batch, shape):
+    torch.manual_seed(42)
+    op = FusedOProjFfnOp(batch, backend="hip", **shape)
+    data = op.gen_data()
+    out = op(*data)
+    ref = torch.from_numpy(oracle.o_proj_ffn(*[n(x) for x in data])).to(out.device)
+    assert op.check(out, ref), (out.float() - ref).norm().item() / ref.norm().item()
+    np.testing.assert_allclose(n(out), n(ref), rtol=5e-2, atol=1e-1)
+
+
+def _layer(batch, seq_len, kwargs, **mode):
+    torch.manual_seed(42)
+    op = Qwen3DenseDecodeOp(batch, seq_len, backend="hip", **kwargs, **mode)
+    data = op.gen_data()
+    K0, V0 = data[1].clone(), data[2].clone()
+    out = op(*data)
+    npy = [n(x) for x in data]
+    extra = {}
+    if mode.get("norm_weights"):
+        extra.update(in_norm_w=npy[7], q_norm_w=npy[8], k_norm_w=npy[9], post_norm_w=npy[10])
+    if mode.get("rope_theta"):
+        extra.update(cos=npy[-2], sin=npy[-1])
+    ref, rK, rV = oracle.qwen3_layer(npy[0], n(K0), n(V0), *npy[3:7], op.num_heads, op.num_kv_heads, op.head_dim,
+                                     kv_lens=mode.get("kv_lens"), **extra)
+    ref_t = torch.from_numpy(ref).to(out.device)
+    assert op.check(out, ref_t), (out.float() - ref_t).norm().item() / ref_t.norm().item()
+    Kc, Vc = data[1], data[2]
+    for b, L in enumerate(op.lens()):
+        np.testing.assert_allclose(n(Kc[b, :, L - 1]), rK[b, :, L - 1], **BF_TOL)
+        np.testing.assert_allclose(n(Vc[b, :, L - 1]), rV[b, :, L - 1], **BF_TOL)
+        mask = torch.ones(seq_len, dtype=torch.bool, device=Kc.device)
+        mask[L - 1] = False
+        assert torch.equal(Kc[b][:, mask], K0[b][:, mask])
+        assert torch.equal(Vc[b][:, mask], V0[b][:, mask])
+
+
+@pytest.mark.parametrize("batch,seq_len,num_kv_heads", [(1, 128, 8), (1, 1000, 8), (2, 1025, 8), (1, 4096, 4), (1, 1, 8)])
+def test_qwen3_dense_decode_reference_mode(batch, seq_len, num_kv_heads):
+    _layer(batch, seq_len, {**QWEN3_VL_2B, "num_kv_heads": num_kv_heads})
+
+
+@pytest.mark.parametrize("batch,seq_len", [(1, 16384), (16, 4096)])
+def test_qwen3_8b_layer_qwen3_mode(batch, seq_len):
+    rng = np.random.default_rng(4)
+    lens = rng.integers(min(1024, seq_len), seq_len + 1, size=batch).tolist()
+    _layer(batch, seq_len, {**QWEN3_8B, "num_kv_heads": 8}, kv_lens=lens, norm_weights=True, rope_theta=1e6)

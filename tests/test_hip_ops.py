@@ -1,0 +1,212 @@
+"""HIP kernels vs the numpy oracle and the golden vectors (GPU).
+
+Bars: bf16 outputs allclose(atol=2e-2, rtol=1e-2) against the fp32-accumulated
+oracle; fp32 RMSNorm 1e-5; fp32 softmax atol 1e-6 /
+rtol 1e-5; sum atol 1e-7 * n (reference ReduceOp tolerance).
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from ezops import AttnDecodeOp, GemvOp, ReduceOp, RmsNormOp, SoftmaxOp, _hip
+from ezops.kernels.gemv.gemv_hip import linear
+from ezops.ops.utils.accuracy import check_determinism, check_input_readonly
+
+pytestmark = pytest.mark.gpu
+BF_TOL = dict(rtol=1e-2, atol=2e-2)
+DEV = "cuda"
+
+
+def n(x):
+    return x.detach().float().cpu().numpy()
+
+
+def g(a, dtype=torch.bfloat16):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dtype).to(DEV)
+
+
+@pytest.mark.parametrize("N,K", [(4096, 4096), (8, 16), (7, 100), (4096, 12288), (6144, 4096), (1, 8), (333, 1032)])
+def test_gemv(N, K):
+    torch.manual_seed(0)
+    op = GemvOp(N, K, backend="hip")
+    A, B, C = op.gen_data()
+    op(A, B, C)
+    np.testing.assert_allclose(n(C), oracle.gemv(n(A), n(B)), **BF_TOL)
+    assert check_determinism(op, (A, B), C) and check_input_readonly(op, (A, B), C)
+
+
+@pytest.mark.parametrize("M", [2, 3, 4, 5, 8, 16, 17, 32])
+@pytest.mark.parametrize("N,K", [(96, 256), (200, 1000), (64, 4096)])
+def test_linear_batched(M, N, K):
+    rng = np.random.default_rng(M * 1000 + N)
+    X = oracle.bf16(rng.standard_normal((M, K)).astype(np.float32))
+    W = oracle.bf16(rng.standard_normal((N, K)).astype(np.float32) * K ** -0.5)
+    Y = linear(g(X), g(W))
+    np.testing.assert_allclose(n(Y), oracle.linear_bf16(X, W), **BF_TOL)
+
+
+@pytest.mark.parametrize("batch,dim", [(1, 64), (128, 1024), (3, 100), (7, 4097), (4096, 4096), (2, 40000)])
+def test_rmsnorm_f32(batch, dim):
+    torch.manual_seed(42)
+    op = RmsNormOp(batch, dim, backend="hip")
+    X, Out = op.gen_data()
+    op(X, Out)
+    ref = torch.from_numpy(oracle.rmsnorm_f32(n(X))).to(DEV)
+    assert op.check(Out, ref), (Out - ref).abs().max().item()
+    assert check_determinism(op, (X,), Out) and check_input_readonly(op, (X,), Out)
+
+
+def test_rmsnorm_f32_custom_eps():
+    torch.manual_seed(42)
+    op = RmsNormOp(64, 1024, backend="hip", eps=1e-5)
+    X, Out = op.gen_data()
+    op(X, Out)
+    assert op.check(Out, torch.from_numpy(oracle.rmsnorm_f32(n(X), 1e-5)).to(DEV))
+
+
+@pytest.mark.parametrize("batch,dim", [(64, 4096), (3, 100), (5, 40000), (1, 8)])
+def test_rmsnorm_bf16_weighted(batch, dim):
+    torch.manual_seed(1)
+    op = RmsNormOp(batch, dim, backend="hip", dtype=torch.bfloat16, weighted=True)
+    X, W, Out = op.gen_data()
+    op(X, W, Out)
+    np.testing.assert_allclose(n(Out), oracle.rmsnorm_bf16(n(X), n(W)), **BF_TOL)
+    assert check_determinism(op, (X, W), Out) and check_input_readonly(op, (X, W), Out)
+
+
+@pytest.mark.parametrize("batch,dim", [(1, 64), (128, 1024), (3, 100), (7, 4097), (64, 32768), (2, 40000)])
+def test_softmax(batch, dim):
+    torch.manual_seed(42)
+    op = SoftmaxOp(batch, dim, backend="hip")
+    X, Out = op.gen_data()
+    X.mul_(3)
+    op(X, Out)
+    ref = torch.from_numpy(oracle.softmax(n(X))).to(DEV)
+    assert op.check(Out, ref), (Out - ref).abs().max().item()
+    assert check_determinism(op, (X,), Out) and check_input_readonly(op, (X,), Out)
+
+
+@pytest.mark.parametrize("size", [1, 37, 1000, (1 << 20) + 3, 1 << 24])
+def test_reduce(size):
+    torch.manual_seed(3)
+    op = ReduceOp(size, backend="hip")
+    A, Out = op.gen_data()
+    op(A, Out)
+    ref = torch.from_numpy(oracle.reduce_sum(n(A))).to(DEV)
+    assert op.check(Out, ref), (Out.item(), ref.item())
+    assert check_determinism(op, (A,), Out) and check_input_readonly(op, (A,), Out)
+
+
+def test_reduce_unaligned_view():
+    base = torch.rand(4097, device=DEV) * 2 - 1
+    A = base[1:]  # 4-byte offset: scalar path
+    op = ReduceOp(4096, backend="hip")
+    Out = torch.empty(1, device=DEV)
+    op(A, Out)
+    assert abs(Out.item() - oracle.reduce_sum(n(A))[0]) <= 1e-7 * 4096
+
+
+@pytest.mark.parametrize("B,H,Hkv,S,D,ragged", [
+    (2, 8, 2, 1, 128, False),      # cache of one slot
+    (1, 32, 8, 1000, 128, False),  # Qwen3-8B heads, non multiple of the tile
+    (2, 16, 8, 1025, 128, False),
+    (3, 8, 8, 300, 64, False),     # MHA, head_dim 64
+    (2, 32, 4, 4097, 128, False),  # group 8
+    (4, 32, 8, 8192, 128, True),   # ragged lengths
+    (3, 16, 8, 700, 64, True),
+])
+def test_attn_decode(B, H, Hkv, S, D, ragged):
+    torch.manual_seed(2)
+    op = AttnDecodeOp(B, H, S, D, backend="hip", num_kv_heads=Hkv)
+    Q, K, V = op.gen_data()
+    lens = None
+    if ragged:
+        lens = torch.randint(1, S + 1, (B,), dtype=torch.int32)
+        lens[0] = S
+        lens = lens.to(DEV)
+    out = op(Q, K, V, lens)
+    ref = oracle.attn_decode(n(Q)[:, :, 0], n(K), n(V), None if lens is None else n(lens).astype(np.int64))
+    np.testing.assert_allclose(n(out)[:, :, 0], ref, **BF_TOL)
+    out2 = op(Q, K, V, lens)  # counters were reset: a second call is identical
+    assert torch.equal(out, out2)
+
+
+def test_attn_decode_stream_and_graph():
+    torch.manual_seed(5)
+    op = AttnDecodeOp(2, 32, 2048, 128, backend="hip", num_kv_heads=8)
+    Q, K, V = op.gen_data()
+    eager = op(Q, K, V)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        g_ = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_, stream=s):
+            out = op(Q, K, V)
+    for _ in range(3):
+        g_.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
+
+# ---- golden vectors through the C ABI
+def test_golden_gemv_rms_softmax_reduce(golden):
+    x, W = golden["gemv_x"], golden["gemv_W"]
+    C = torch.empty(W.shape[0], dtype=torch.bfloat16, device=DEV)
+    GemvOp(*W.shape, backend="hip")(g(x), g(W), C)
+    np.testing.assert_allclose(n(C), golden["gemv_y"], **BF_TOL)
+    X = g(golden["rms32_X"], torch.float32)
+    O = torch.empty_like(X)
+    RmsNormOp(*X.shape, backend="hip")(X, O)
+    np.testing.assert_allclose(n(O), golden["rms32_out"], rtol=1e-5, atol=1e-6)
+    X, w = g(golden["rmsbf_X"]), g(golden["rmsbf_w"])
+    O = torch.empty_like(X)
+    RmsNormOp(*X.shape, backend="hip", dtype=torch.bfloat16, weighted=True)(X, w, O)
+    np.testing.assert_allclose(n(O), golden["rmsbf_out"], **BF_TOL)
+    X = g(golden["softmax_X"], torch.float32)
+    O = torch.empty_like(X)
+    SoftmaxOp(*X.shape, backend="hip")(X, O)
+    np.testing.assert_allclose(n(O), golden["softmax_out"], rtol=1e-5, atol=1e-6)
+    A = g(golden["reduce_A"], torch.float32)
+    O = torch.empty(1, device=DEV)
+    ReduceOp(A.numel(), backend="hip")(A, O)
+    np.testing.assert_allclose(n(O), golden["reduce_out"], atol=1e-7 * A.numel())
+
+
+def test_golden_o_proj_ffn_through_abi(golden):
+    gd = golden
+    attn, res = g(gd["ffn_attn"]), g(gd["ffn_res"])
+    Wo, w, Wg, Wu, Wd = (g(gd[k]) for k in ("ffn_Wo", "ffn_w", "ffn_Wg", "ffn_Wu", "ffn_Wd"))
+    B, QR = attn.shape
+    HS, IS = Wo.shape[0], Wg.shape[0]
+    out = torch.empty(B, HS, dtype=torch.bfloat16, device=DEV)
+    ws = torch.zeros(_hip.size("ezops_o_proj_ffn_workspace_size", B, HS, IS, QR), dtype=torch.uint8, device=DEV)
+    _hip.call("ezops_o_proj_ffn_bf16", attn.data_ptr(), res.data_ptr(), Wo.data_ptr(), w.data_ptr(), Wg.data_ptr(),
+              Wu.data_ptr(), Wd.data_ptr(), out.data_ptr(), B, HS, IS, QR, 1e-6, ws.data_ptr(), ws.numel(),
+              _hip.stream())
+    np.testing.assert_allclose(n(out), gd["ffn_out"], **BF_TOL)
+
+
+def test_golden_qk_norm_rope_through_abi(golden):
+    gd = golden
+    q, k, v = g(gd["rope_q"]), g(gd["rope_k"]), g(gd["rope_v"])
+    B, H, D = q.shape
+    Hkv, S = k.shape[1], gd["rope_cos"].shape[0]
+    Kc, Vc = g(gd["rope_Kc"]), g(gd["rope_Vc"])
+    qo = torch.empty_like(q)
+    ko = torch.empty_like(k)
+    pos = torch.from_numpy(gd["rope_pos"]).to(DEV)
+    # keep every operand referenced until the kernel has run
+    qw, kw, cos, sin = (g(gd[k_]) for k_ in ("rope_qw", "rope_kw", "rope_cos", "rope_sin"))
+    _hip.call("ezops_qk_norm_rope_bf16", q.data_ptr(), H * D, k.data_ptr(), Hkv * D, v.data_ptr(), Hkv * D,
+              qw.data_ptr(), kw.data_ptr(), cos.data_ptr(), sin.data_ptr(), Kc.data_ptr(), Vc.data_ptr(),
+              qo.data_ptr(), ko.data_ptr(),
+              B, H, Hkv, D, S, 0, pos.data_ptr(), 0, 1e-6, _hip.stream())
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(n(qo), gd["rope_qout"], **BF_TOL)
+    np.testing.assert_allclose(n(ko), gd["rope_kout"], **BF_TOL)
+    for b, p in enumerate(gd["rope_pos"]):
+        np.testing.assert_array_equal(n(Vc)[b, :, p], gd["rope_v"][b])
+        np.testing.assert_array_equal(n(Kc)[b, :, p], n(ko)[b])

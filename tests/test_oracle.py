@@ -1,0 +1,182 @@
+"""Pins of the numpy oracle against independent checks (CPU only).
+
+Each oracle function is checked against a library routine (torch CPU), a
+brute-force loop, or an invariant that a dropped term, a wrong sign or a
+transposed operand would break.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+
+
+def t(a):
+    return torch.from_numpy(np.ascontiguousarray(a))
+
+
+def bfr(rng, *shape, scale=1.0, mean=0.0):
+    return oracle.bf16(rng.standard_normal(shape).astype(np.float32) * scale + mean)
+
+
+def test_bf16_matches_torch_including_specials():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.standard_normal(10000).astype(np.float32) * 1e3,
+        np.array([0.0, -0.0, np.inf, -np.inf, 3.0e38, -3.0e38, 1e-40, 1.00390625, 1.01171875], np.float32),
+        # exact ties: 1 + 2^-8 rounds to even (down), 1 + 3*2^-8 rounds up
+        np.array([1 + 2 ** -8, 1 + 3 * 2 ** -8, -(1 + 2 ** -8)], np.float32),
+    ])
+    a = oracle.bf16(x)
+    b = t(x).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.isnan(oracle.bf16(np.array([np.nan], np.float32)))[0]
+
+
+def test_gemv_brute_force_and_torch_mv():
+    rng = np.random.default_rng(1)
+    x, W = bfr(rng, 33), bfr(rng, 7, 33, scale=0.3)
+    y = oracle.gemv(x, W)
+    brute = [sum(float(W[n, k]) * float(x[k]) for k in range(33)) for n in range(7)]
+    np.testing.assert_allclose(y, oracle.bf16(np.array(brute, np.float32)), rtol=8e-3, atol=1e-6)
+    ref = torch.mv(t(W).double(), t(x).double()).float().to(torch.bfloat16).float().numpy()
+    np.testing.assert_allclose(y, ref, rtol=8e-3)
+    # transposed weight must not pass
+    assert not np.allclose(oracle.gemv(x[:7], W[:, :7].T.copy()), oracle.gemv(x[:7], W[:, :7]), rtol=1e-2)
+
+
+def test_rmsnorm_f32_vs_torch_and_unit_rms():
+    rng = np.random.default_rng(2)
+    X = rng.standard_normal((5, 100)).astype(np.float32) * 3
+    y = oracle.rmsnorm_f32(X, 1e-6)
+    ref = F.rms_norm(t(X).double(), (100,), eps=1e-6).float().numpy()
+    np.testing.assert_allclose(y, ref, rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(np.sqrt(np.mean(y.astype(np.float64) ** 2, -1)), 1.0, rtol=1e-5)
+
+
+def test_rmsnorm_bf16_weighted_vs_torch():
+    rng = np.random.default_rng(3)
+    X, w = bfr(rng, 4, 64), bfr(rng, 64, scale=0.1, mean=1.0)
+    y = oracle.rmsnorm_bf16(X, w, 1e-6)
+    ref = F.rms_norm(t(X).double(), (64,), weight=t(w).double(), eps=1e-6).float().numpy()
+    np.testing.assert_allclose(y, ref, rtol=8e-3, atol=1e-6)
+    assert np.array_equal(y, oracle.bf16(y))
+
+
+def test_softmax_vs_torch_and_sum_to_one():
+    rng = np.random.default_rng(4)
+    X = rng.standard_normal((6, 333)).astype(np.float32) * 3
+    y = oracle.softmax(X)
+    np.testing.assert_allclose(y, torch.softmax(t(X).double(), -1).float().numpy(), rtol=1e-6, atol=1e-9)
+    np.testing.assert_allclose(y.astype(np.float64).sum(-1), 1.0, rtol=1e-6)
+    assert (y > 0).all() and (y <= 1).all()
+
+
+def test_reduce_sum_vs_fsum():
+    rng = np.random.default_rng(5)
+    A = rng.uniform(-1, 1, 100001).astype(np.float32)
+    assert oracle.reduce_sum(A)[0] == np.float32(math.fsum(float(a) for a in A))
+    # permutation invariance of the (exact-then-rounded) oracle
+    assert oracle.reduce_sum(A[::-1])[0] == oracle.reduce_sum(A)[0]
+
+
+@pytest.mark.parametrize("B,H,Hkv,S,D", [(2, 8, 2, 37, 64), (1, 4, 4, 5, 16), (3, 8, 1, 9, 32)])
+def test_attn_vs_torch_sdpa_math(B, H, Hkv, S, D):
+    rng = np.random.default_rng(6)
+    Q, K, V = bfr(rng, B, H, D), bfr(rng, B, Hkv, S, D), bfr(rng, B, Hkv, S, D)
+    y = oracle.attn_decode(Q, K, V)
+    with torch.nn.attention.sdpa_kernel([torch.nn.attention.SDPBackend.MATH]):
+        ref = F.scaled_dot_product_attention(t(Q).double()[:, :, None], t(K).double(), t(V).double(),
+                                             enable_gqa=True)[:, :, 0]
+    np.testing.assert_allclose(y, oracle.bf16(ref.float().numpy()), rtol=1e-2, atol=1e-2)
+    # output per dim lies inside the range of the values attended
+    G = H // Hkv
+    Vmin = np.repeat(V.min(2), G, axis=1)
+    Vmax = np.repeat(V.max(2), G, axis=1)
+    assert (y >= Vmin - 1e-2).all() and (y <= Vmax + 1e-2).all()
+
+
+def test_attn_invariants():
+    rng = np.random.default_rng(7)
+    B, H, Hkv, S, D = 2, 4, 2, 11, 16
+    Q, K, V = bfr(rng, B, H, D), bfr(rng, B, Hkv, S, D), bfr(rng, B, Hkv, S, D)
+    # a single slot returns its value exactly
+    one = oracle.attn_decode(Q, K[:, :, :1], V[:, :, :1])
+    np.testing.assert_array_equal(one, np.repeat(V[:, :, 0], 2, axis=1))
+    # kv_lens equals truncating the cache
+    lens = np.array([11, 4])
+    y = oracle.attn_decode(Q, K, V, lens)
+    np.testing.assert_array_equal(y[1], oracle.attn_decode(Q[1:], K[1:, :, :4], V[1:, :, :4])[0])
+    np.testing.assert_array_equal(y[0], oracle.attn_decode(Q[:1], K[:1], V[:1])[0])
+    # GQA equals MHA on an expanded cache
+    mha = oracle.attn_decode(Q, np.repeat(K, 2, axis=1), np.repeat(V, 2, axis=1))
+    np.testing.assert_allclose(oracle.attn_decode(Q, K, V), mha, rtol=1e-6)
+
+
+def test_rope_tables_vs_torch():
+    cos, sin = oracle.rope_tables(64, 32, 1e6)
+    inv = 1.0 / (1e6 ** (torch.arange(0, 32, 2, dtype=torch.float32) / 32))
+    ang = torch.arange(64, dtype=torch.float32)[:, None] * inv[None, :]
+    tc = torch.cat([ang.cos(), ang.cos()], -1).to(torch.bfloat16).float().numpy()
+    ts = torch.cat([ang.sin(), ang.sin()], -1).to(torch.bfloat16).float().numpy()
+    assert np.abs(cos - tc).max() <= 2 ** -8 and np.abs(sin - ts).max() <= 2 ** -8
+    assert (cos[0] == 1).all() and (sin[0] == 0).all()
+
+
+def test_qk_norm_rope_properties():
+    rng = np.random.default_rng(8)
+    B, H, Hkv, D, S = 2, 4, 2, 16, 9
+    q, k, v = bfr(rng, B, H, D), bfr(rng, B, Hkv, D), bfr(rng, B, Hkv, D)
+    ones = np.ones(D, np.float32)
+    cos, sin = oracle.rope_tables(S, D, 1e4)
+    Kc, Vc = bfr(rng, B, Hkv, S, D), bfr(rng, B, Hkv, S, D)
+    # position 0 is the identity rotation: equals plain per-head RMSNorm
+    q0, k0, _, _ = oracle.qk_norm_rope(q, k, v, ones, ones, cos, sin, Kc, Vc, 0)
+    np.testing.assert_array_equal(q0, oracle.rmsnorm_bf16(q.reshape(-1, D)).reshape(B, H, D))
+    # rotation keeps the norm of each (i, i + D/2) pair
+    pos = np.array([3, 8])
+    q1, k1, Kn, Vn = oracle.qk_norm_rope(q, k, v, ones, ones, cos, sin, Kc, Vc, pos)
+    n0 = np.hypot(q0[..., :D // 2], q0[..., D // 2:])
+    n1 = np.hypot(q1[..., :D // 2], q1[..., D // 2:])
+    np.testing.assert_allclose(n1, n0, rtol=2e-2, atol=2e-2)
+    # only the written slot changes; v is copied bit-exactly
+    for b in range(B):
+        mask = np.ones(S, bool)
+        mask[pos[b]] = False
+        np.testing.assert_array_equal(Kn[b][:, mask], Kc[b][:, mask])
+        np.testing.assert_array_equal(Vn[b, :, pos[b]], v[b])
+        np.testing.assert_array_equal(Kn[b, :, pos[b]], k1[b])
+    # sign convention: x[i]*cos - x[i+h]*sin for the first half
+    x = np.zeros((1, 1, D), np.float32)
+    x[0, 0, D // 2] = 1.0
+    qr, _, _, _ = oracle.qk_norm_rope(x, x[:, :1] * 0 + 1, x[:, :1], ones, ones, cos, sin,
+                                      np.zeros((1, 1, S, D), np.float32), np.zeros((1, 1, S, D), np.float32), 2)
+    r = math.sqrt(D / (1 + 1e-6 * D))
+    assert qr[0, 0, 0] == oracle.bf16(np.float32(-r * sin[2, 0]))
+
+
+def test_qwen3_layer_reference_mode_composition():
+    """Reference mode (no kv_lens/weights/RoPE) equals composing the pinned pieces."""
+    rng = np.random.default_rng(9)
+    B, HS, IS, H, Hkv, D, S = 2, 32, 48, 4, 2, 8, 5
+    QR, KVR = H * D, Hkv * D
+    hid = bfr(rng, B, HS)
+    Kc, Vc = bfr(rng, B, Hkv, S, D), bfr(rng, B, Hkv, S, D)
+    Wqkv, Wo = bfr(rng, QR + 2 * KVR, HS, scale=HS ** -0.5), bfr(rng, HS, QR, scale=QR ** -0.5)
+    Wgu, Wd = bfr(rng, 2 * IS, HS, scale=HS ** -0.5), bfr(rng, HS, IS, scale=IS ** -0.5)
+    out, Kn, Vn = oracle.qwen3_layer(hid, Kc, Vc, Wqkv, Wo, Wgu, Wd, H, Hkv, D)
+    qkv = oracle.linear_bf16(oracle.rmsnorm_bf16(hid), Wqkv)
+    q = oracle.rmsnorm_bf16(qkv[:, :QR].reshape(-1, D)).reshape(B, H, D)
+    k = oracle.rmsnorm_bf16(qkv[:, QR:QR + KVR].reshape(-1, D)).reshape(B, Hkv, D)
+    np.testing.assert_array_equal(Kn[:, :, -1], k)
+    np.testing.assert_array_equal(Vn[:, :, -1], qkv[:, QR + KVR:].reshape(B, Hkv, D))
+    att = oracle.attn_decode(q, Kn, Vn).reshape(B, QR)
+    h = oracle.bf16(hid + oracle.linear_bf16(att, Wo))
+    xn = oracle.rmsnorm_bf16(h)
+    gu = oracle.linear_bf16(xn, Wgu)
+    ff = oracle.linear_bf16(oracle.bf16(oracle.bf16(gu[:, :IS] / (1 + np.exp(-gu[:, :IS].astype(np.float64)))) * gu[:, IS:]), Wd)
+    np.testing.assert_allclose(out, oracle.bf16(h + ff), rtol=1e-2, atol=1e-2)
