@@ -36,9 +36,9 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
-def _compile(src: Path) -> Path:
-    obj = BUILD / (src.name + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, build_dir: Path = BUILD, extra: tuple = ()) -> Path:
+    obj = build_dir / (src.name + ".o")
+    cmd = [hipcc(), *HIPCC_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     if src.suffix == ".cpp":
         cmd = [hipcc(), "-O3", "-std=c++17", "-fPIC", "-Wall", "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -51,25 +51,31 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-def build(jobs: int | None = None, verbose: bool = True) -> Path:
-    BUILD.mkdir(parents=True, exist_ok=True)
-    LIB.parent.mkdir(parents=True, exist_ok=True)
+def build(jobs: int | None = None, verbose: bool = True, extra_flags: tuple = (), lib: Path = LIB,
+          build_dir: Path = BUILD) -> Path:
+    """Compile csrc/ into ``lib``; ``extra_flags`` (e.g. tile-size -D macros) go to every hipcc call."""
+    build_dir.mkdir(parents=True, exist_ok=True)
+    lib.parent.mkdir(parents=True, exist_ok=True)
     sources = sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
     jobs = jobs or min(8, os.cpu_count() or 1)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, sources))
-    tmp = LIB.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda src: _compile(src, build_dir, tuple(extra_flags)), sources))
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}{r.stderr}")
-    os.replace(tmp, LIB)  # atomic: a concurrent loader never sees a half-written file
+    os.replace(tmp, lib)  # atomic: a concurrent loader never sees a half-written file
     if verbose:
-        print(f"built {LIB} from {len(sources)} sources")
-    return LIB
+        print(f"built {lib} from {len(sources)} sources")
+    return lib
 
 
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("-j", type=int, default=None)
-    build(ap.parse_args().j)
+    ap.add_argument("-D", action="append", default=[], help="extra preprocessor definition (variant builds)")
+    ap.add_argument("-o", type=Path, default=LIB, help="output library path")
+    args = ap.parse_args()
+    bdir = BUILD if args.o == LIB else args.o.parent / "_build"
+    build(args.j, extra_flags=tuple(f"-D{d}" for d in args.D), lib=args.o, build_dir=bdir)

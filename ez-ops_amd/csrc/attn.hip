@@ -25,9 +25,13 @@ namespace {
 
 constexpr int kAttnBlock = 256;
 constexpr int kAttnWaves = 4;
-constexpr int kTile = 64;           // positions per wave iteration
+#ifndef EZ_ATTN_TILE
+#define EZ_ATTN_TILE 32
+#endif
+constexpr int kTile = EZ_ATTN_TILE;  // positions per wave iteration
 constexpr int kMinChunk = kTile * kAttnWaves;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kMaxSplits = 64;  // one wave reads all split statistics in the merge
 
 int num_cus() {
   static int cus = 0;
@@ -50,6 +54,7 @@ SplitPlan plan_splits(int64_t B, int64_t Hkv, int64_t S) {
   int64_t ns = (target + units - 1) / units;
   const int64_t max_ns = (S + kMinChunk - 1) / kMinChunk;
   if (ns > max_ns) ns = max_ns;
+  if (ns > kMaxSplits) ns = kMaxSplits;
   if (ns < 1) ns = 1;
   int64_t chunk = (S + ns - 1) / ns;
   chunk = (chunk + kTile - 1) / kTile * kTile;
@@ -65,6 +70,37 @@ struct AttnWs {
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
+// K rows enter the MFMA B operand with k-slot (lg, e) of sub-step s mapped to
+// head dim s*32 + lg*8 + e: one wave load instruction then reads, for each of
+// its 16 positions, 64 contiguous bytes (4 lanes x 16 B).  The Q operand uses
+// the same mapping, so the contraction is unchanged.
+template <int D, int NSUB>
+__device__ __forceinline__ void load_k_tile(const uint16_t* Kb, int64_t t0, int64_t last, int li, int lg,
+                                            uint4 (&kf)[NSUB][D / 32]) {
+#pragma unroll
+  for (int u = 0; u < NSUB; ++u) {
+    int64_t p = t0 + 16 * u + li;
+    p = p < last ? p : last;
+    const uint16_t* row = Kb + p * D + lg * 8;
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s) kf[u][s] = ld16_stream(row + 32 * s);
+  }
+}
+
+// V rows in row layout: lane (dc, rs) reads rows rs, rs + RPI, ... of the tile,
+// 16 B at column 8*dc; one wave instruction covers RPI consecutive rows.
+template <int D, int NPV>
+__device__ __forceinline__ void load_v_tile(const uint16_t* Vb, int64_t t0, int64_t last, int dc, int rs,
+                                            uint4 (&vf)[NPV]) {
+  constexpr int RPI = kWave / (D / 8);
+#pragma unroll
+  for (int j = 0; j < NPV; ++j) {
+    int64_t p = t0 + rs + RPI * j;
+    p = p < last ? p : last;
+    vf[j] = ld16_stream(Vb + p * D + dc * 8);
+  }
+}
+
 template <int D, int G>
 __global__ __launch_bounds__(kAttnBlock) void attn_split_kernel(AttnArgs a, int64_t nsplit,
                                                                int64_t chunk, AttnWs ws) {
@@ -79,6 +115,7 @@ __global__ __launch_bounds__(kAttnBlock) void attn_split_kernel(AttnArgs a, int6
   __shared__ __align__(16) float Ps[kAttnWaves][kTile][GP];
   __shared__ __align__(16) float Os[kAttnWaves][G][D];
   __shared__ float Ms[kAttnWaves][G], Ls[kAttnWaves][G];
+  __shared__ float Wt[G][kMaxSplits];
 
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
@@ -89,18 +126,27 @@ __global__ __launch_bounds__(kAttnBlock) void attn_split_kernel(AttnArgs a, int6
   L = L < 0 ? 0 : (L > a.S ? a.S : L);
   const int64_t p_begin = split * chunk;
   const int64_t p_end = (p_begin + chunk < L) ? p_begin + chunk : L;
+  const int64_t last = p_end - 1;
 
   const uint16_t* Kb = a.K + (b * a.Hkv + kvh) * a.S * D;
   const uint16_t* Vb = a.V + (b * a.Hkv + kvh) * a.S * D;
   const int64_t h0 = kvh * G;  // first query head of the group
   const float sl2 = a.scale * kLog2e;
+  const int dc = lane % CPR, rs = lane / CPR;
 
-  // Q operand: lane (li, lg) holds Q[h0 + li][lg*(D/4) + 8s .. +8] for step s.
+  int64_t t0 = p_begin + int64_t(wave) * kTile;
+  uint4 kf[NSUB][NS], vf[NPV];
+  if (t0 < p_end) {
+    load_k_tile<D, NSUB>(Kb, t0, last, li, lg, kf);
+    load_v_tile<D, NPV>(Vb, t0, last, dc, rs, vf);
+  }
+
+  // Q operand: lane (li, lg) holds Q[h0 + li][s*32 + lg*8 .. +8] for step s.
   bf16x8_t qf[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     uint4 v = make_uint4(0, 0, 0, 0);
-    if (li < G) v = *reinterpret_cast<const uint4*>(a.Q + ((b * a.H + h0 + li) * D) + lg * (D / 4) + 8 * s);
+    if (li < G) v = *reinterpret_cast<const uint4*>(a.Q + ((b * a.H + h0 + li) * D) + 32 * s + lg * 8);
     qf[s] = as_bf16x8(v);
   }
 
@@ -112,28 +158,9 @@ __global__ __launch_bounds__(kAttnBlock) void attn_split_kernel(AttnArgs a, int6
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
   }
-  const int dc = lane % CPR, rs = lane / CPR;
 
-  for (int64_t t0 = p_begin + int64_t(wave) * kTile; t0 < p_end; t0 += int64_t(kAttnWaves) * kTile) {
-    const int64_t last = p_end - 1;
-    // ---- issue K (MFMA operand layout) and V (row layout) loads
-    uint4 kf[NSUB][NS];
-#pragma unroll
-    for (int u = 0; u < NSUB; ++u) {
-      int64_t p = t0 + 16 * u + li;
-      p = p < last ? p : last;
-#pragma unroll
-      for (int s = 0; s < NS; ++s)
-        kf[u][s] = *reinterpret_cast<const uint4*>(Kb + p * D + lg * (D / 4) + 8 * s);
-    }
-    uint4 vf[NPV];
-#pragma unroll
-    for (int j = 0; j < NPV; ++j) {
-      int64_t p = t0 + rs + RPI * j;
-      p = p < last ? p : last;
-      vf[j] = *reinterpret_cast<const uint4*>(Vb + p * D + dc * 8);
-    }
-
+  for (; t0 < p_end; t0 += int64_t(kAttnWaves) * kTile) {
+    const int64_t tn = t0 + int64_t(kAttnWaves) * kTile;
     // ---- scores: acc[u][j] = S[head 4*lg + j][pos t0 + 16u + li]
     f32x4_t acc[NSUB];
 #pragma unroll
@@ -143,6 +170,8 @@ __global__ __launch_bounds__(kAttnBlock) void attn_split_kernel(AttnArgs a, int6
       for (int s = 0; s < NS; ++s)
         acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf[s], as_bf16x8(kf[u][s]), acc[u], 0, 0, 0);
     }
+    if (tn < p_end) load_k_tile<D, NSUB>(Kb, tn, last, li, lg, kf);  // next K while this tile finishes
+
     float mx[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -154,7 +183,7 @@ __global__ __launch_bounds__(kAttnBlock) void attn_split_kernel(AttnArgs a, int6
         acc[u][j] = sv;
         mx[j] = fmaxf(mx[j], sv);
       }
-      mx[j] = row16_max(mx[j]);
+      mx[j] = dpp_row16<true>(mx[j]);
     }
     // ---- wave-uniform running max and rescale factors
     float m_use[G];
@@ -205,6 +234,7 @@ __global__ __launch_bounds__(kAttnBlock) void attn_split_kernel(AttnArgs a, int6
         for (int e = 0; e < 8; ++e) o[h][e] = fmaf(pr[h], v[e], o[h][e]);
       }
     }
+    if (tn < p_end) load_v_tile<D, NPV>(Vb, tn, last, dc, rs, vf);  // next V
     __builtin_amdgcn_wave_barrier();
   }
 
@@ -251,32 +281,49 @@ __global__ __launch_bounds__(kAttnBlock) void attn_split_kernel(AttnArgs a, int6
     if (nsplit == 1) {
       a.Out[hq * D + d] = f2bf(lv > 0.f ? ov / lv : 0.f);
     } else {
-      ws.opart[(hq * nsplit + split) * D + d] = ov;
+      st_dev(ws.opart + (hq * nsplit + split) * D + d, ov);
       if (d == 0) {
-        ws.ml[(hq * nsplit + split) * 2 + 0] = M;
-        ws.ml[(hq * nsplit + split) * 2 + 1] = lv;
+        st_dev(ws.ml + (hq * nsplit + split) * 2 + 0, M);
+        st_dev(ws.ml + (hq * nsplit + split) * 2 + 1, lv);
       }
     }
   }
   if (nsplit == 1) return;
   if (!arrive_last(ws.counters + unit, int(nsplit))) return;
 
-  // ---- last block of the unit merges the splits
+  // ---- last block of the unit merges the splits.
+  // (1) per head: one wave reads the nsplit (max, sum) pairs at once and
+  //     turns them into normalised weights w_s = 2^(m_s - M) / sum_s' ...
+  for (int h = wave; h < G; h += kAttnWaves) {
+    const int64_t hq = b * a.H + h0 + h;
+    const float* ml = ws.ml + hq * nsplit * 2;
+    const bool ok = lane < nsplit;
+    const float ms = ok ? ld_dev(ml + 2 * lane) : -INFINITY;
+    const float ls = ok ? ld_dev(ml + 2 * lane + 1) : 0.f;
+    const float M = wave_reduce_uniform<true>(ms);
+    const float f = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
+    const float tot = wave_reduce_uniform<false>(f * ls);
+    if (ok) Wt[h][lane] = tot > 0.f ? f / tot : 0.f;
+  }
+  __syncthreads();
+  // (2) thread per (h, d): weighted sum of the split partials, loads issued
+  //     eight at a time.
   for (int idx = threadIdx.x; idx < G * D; idx += kAttnBlock) {
     const int h = idx / D, d = idx % D;
     const int64_t hq = b * a.H + h0 + h;
-    const float* ml = ws.ml + hq * nsplit * 2;
     const float* op = ws.opart + hq * nsplit * D + d;
-    float M = -INFINITY;
-    for (int64_t s = 0; s < nsplit; ++s) M = fmaxf(M, ml[2 * s]);
-    float ov = 0.f, lv = 0.f;
-    for (int64_t s = 0; s < nsplit; ++s) {
-      const float ms = ml[2 * s];
-      const float f = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
-      ov = fmaf(f, op[s * D], ov);
-      lv = fmaf(f, ml[2 * s + 1], lv);
+    float acc8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int64_t s0 = 0;
+    for (; s0 + 8 <= nsplit; s0 += 8) {
+      float v8[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v8[e] = ld_dev(op + (s0 + e) * D);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc8[e] = fmaf(Wt[h][s0 + e], v8[e], acc8[e]);
     }
-    a.Out[hq * D + d] = f2bf(lv > 0.f ? ov / lv : 0.f);
+    for (; s0 < nsplit; ++s0) acc8[0] = fmaf(Wt[h][s0], ld_dev(op + s0 * D), acc8[0]);
+    const float r = ((acc8[0] + acc8[1]) + (acc8[2] + acc8[3])) + ((acc8[4] + acc8[5]) + (acc8[6] + acc8[7]));
+    a.Out[hq * D + d] = f2bf(r);
   }
 }
 

@@ -4,6 +4,10 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#ifndef EZ_NT_LOADS
+#define EZ_NT_LOADS 0
+#endif
+
 namespace ez {
 
 constexpr int kWave = 64;
@@ -40,6 +44,19 @@ __device__ __forceinline__ void unpack8(const uint4& v, float (&f)[8]) {
   f[6] = bf_lo(v.w); f[7] = bf_hi(v.w);
 }
 
+// 16-byte global load; with EZ_NT_LOADS the load carries the non-temporal
+// hint (streamed weights / KV are read once and should not displace reused
+// lines).
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld16_stream(const void* p) {
+#if EZ_NT_LOADS
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+#else
+  return *reinterpret_cast<const uint4*>(p);
+#endif
+}
+
 __device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& v) { return __builtin_bit_cast(bf16x8_t, v); }
 
 // ---- wave / block reductions (fixed butterfly order => deterministic,
@@ -66,6 +83,37 @@ __device__ __forceinline__ float row16_max(float v) {
   return v;
 }
 
+// DPP reductions inside each 16-lane row: quad_perm [1,0,3,2], quad_perm
+// [2,3,0,1], row_half_mirror, row_mirror.  Every lane of the row ends with the
+// row's result (the combination order is the same for all lanes up to
+// commutation, so the values are bit-identical).
+template <bool MAX>
+__device__ __forceinline__ float dpp_row16(float v) {
+#define EZ_DPP_STEP(ctrl)                                                                 \
+  {                                                                                       \
+    const float o = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, true)); \
+    v = MAX ? fmaxf(v, o) : v + o;                                                        \
+  }
+  EZ_DPP_STEP(0xB1)
+  EZ_DPP_STEP(0x4E)
+  EZ_DPP_STEP(0x141)
+  EZ_DPP_STEP(0x140)
+#undef EZ_DPP_STEP
+  return v;
+}
+
+// Wave-uniform sum/max: DPP inside the four 16-lane rows, then the four row
+// results combined in a fixed order through readlane.
+template <bool MAX>
+__device__ __forceinline__ float wave_reduce_uniform(float v) {
+  v = dpp_row16<MAX>(v);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return MAX ? fmaxf(fmaxf(r0, r1), fmaxf(r2, r3)) : (r0 + r1) + (r2 + r3);
+}
+
 // Block-wide reduction; `red` must hold NWAVES floats of LDS.  Every thread
 // gets the result.  Contains __syncthreads().
 template <int NWAVES, bool MAX>
@@ -87,24 +135,39 @@ __device__ __forceinline__ float block_reduce(float v, float* red) {
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
 
-// Device-scope arrival counter used by "last block finishes" reductions.
-// Release the block's prior global writes, count the arrival, and report
-// whether this block is the last of `expected`.  The last block resets the
-// counter to zero so the next launch (or graph replay) starts clean.
+// ---- cross-block hand-off without cache maintenance ---------------------
+// gfx950 has one L2 per XCD and the L2s are not coherent with each other.
+// A device-scope fence (__threadfence) therefore writes back and
+// invalidates the whole L2 of the XCD (buffer_wbl2 / buffer_inv), which costs
+// about a microsecond and serialises per XCD.  Data handed from one block to
+// another is instead written and read with device-scope atomic accesses
+// (global_store/global_load with the sc1 bit), which are coherent at device
+// scope by themselves; only completion ordering is then needed.
+__device__ __forceinline__ void st_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Arrival counter for "last block finishes" reductions.  Precondition: every
+// thread's hand-off data was written with st_dev.  Waits until those stores
+// have completed, counts the block's arrival, and tells every thread whether
+// this block is the last of `expected`.  The last block resets the counter
+// to zero, so the next launch (or graph replay) starts clean.  The last
+// block must read the hand-off data with ld_dev.
 __device__ __forceinline__ bool arrive_last(int* counter, int expected) {
   __shared__ int s_last;
-  __syncthreads();
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's sc1 stores are complete
+  __syncthreads();                 // ... and so are every other thread's
   if (threadIdx.x == 0) {
-    __threadfence();
-    int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    int last = (prev == expected - 1);
+    const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = prev == expected - 1;
     if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = last;
   }
   __syncthreads();
-  bool last = s_last != 0;
-  if (last) __threadfence();
-  return last;
+  return s_last != 0;
 }
 
 }  // namespace ez

@@ -16,11 +16,24 @@
 #include "status.h"
 #include "../../include/ezops_hip.h"
 
+// Tunables (defaults chosen by measurement on MI355X).
+#ifndef EZ_GEMV_BLOCK
+#define EZ_GEMV_BLOCK 256   // threads per block of the VALU GEMV
+#endif
+#ifndef EZ_GEMV_R1
+#define EZ_GEMV_R1 2        // weight rows per wave when M == 1
+#endif
+#ifndef EZ_GEMV_U
+#define EZ_GEMV_U 8         // 16-byte chunks per lane in flight per row (M <= 2)
+#endif
+
 namespace ez {
 namespace {
 
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
+constexpr int kGemvBlock = EZ_GEMV_BLOCK;
+constexpr int kGemvWaves = kGemvBlock / kWave;
 
 __device__ __forceinline__ void store_out(const LinearArgs& a, int64_t m, int64_t n, float v,
                                           float v_up) {
@@ -44,9 +57,9 @@ __device__ __forceinline__ void store_out(const LinearArgs& a, int64_t m, int64_
 // (kEpiSilu: R = 2 with gate row n and up row n).  U chunks per lane are in
 // flight per loop trip.
 template <int M, int R, int U, bool NORM, bool SILU>
-__global__ __launch_bounds__(kBlock) void gemv_valu_kernel(LinearArgs a) {
+__global__ __launch_bounds__(kGemvBlock) void gemv_valu_kernel(LinearArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t wrow = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  const int64_t wrow = int64_t(blockIdx.x) * kGemvWaves + (threadIdx.x >> 6);
   const int64_t n0 = SILU ? wrow : wrow * R;
   if (n0 >= a.N) return;
 
@@ -80,7 +93,7 @@ __global__ __launch_bounds__(kBlock) void gemv_valu_kernel(LinearArgs a) {
       const int64_t c = c0 + int64_t(kWave) * u;
       const bool ok = c < nchunk;
 #pragma unroll
-      for (int r = 0; r < R; ++r) wv[u][r] = ok ? wp[r][c] : make_uint4(0, 0, 0, 0);
+      for (int r = 0; r < R; ++r) wv[u][r] = ok ? ld16_stream(wp[r] + c) : make_uint4(0, 0, 0, 0);
 #pragma unroll
       for (int m = 0; m < M; ++m) xv[u][m] = ok ? xp[m][c] : make_uint4(0, 0, 0, 0);
       if (NORM) nv[u] = (ok && nwp) ? nwp[c] : make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
@@ -139,9 +152,10 @@ __global__ __launch_bounds__(kBlock) void gemv_valu_kernel(LinearArgs a) {
 //   A (weights):  A[i][g*8 .. g*8+7]   = W[row0 + i][k(g, s, 0..7)]
 //   B (batch):    B[g*8 .. g*8+7][i]   = X[m0 + i][k(g, s, 0..7)]
 //   C:            C[4*g + j][i], j = 0..3  -> weight row row0+4g+j, batch m0+i
-// The k-slot assignment k(g, s, e) = k0 + 32*g + 8*s + e (s = sub-step 0..3
+// The k-slot assignment k(g, s, e) = k0 + 32*s + 8*g + e (s = sub-step 0..3
 // of a 128-wide chunk) is the same for A and B, so the contraction is
-// exact, and each lane reads 64 contiguous bytes of its weight row per chunk.
+// exact, and each wave load instruction reads 64 contiguous bytes (4 lanes)
+// of each of its 16 weight rows.
 template <int T, bool NORM, bool SILU>
 __global__ __launch_bounds__(kBlock) void linear_mfma_kernel(LinearArgs a) {
   __shared__ float red[kWavesPerBlock][T][4][kWave];
@@ -172,21 +186,21 @@ __global__ __launch_bounds__(kBlock) void linear_mfma_kernel(LinearArgs a) {
   float ss = 0.f;
 
   for (int64_t c = cb; c < ce; ++c) {
-    const int64_t kb = c * 128 + g * 32;
+    const int64_t kb = c * 128 + g * 8;
     uint4 wv[T][4], xv[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const int64_t k = kb + s * 8;
+      const int64_t k = kb + s * 32;
       const bool ok = k < a.K;
 #pragma unroll
       for (int t = 0; t < T; ++t)
-        wv[t][s] = ok ? *reinterpret_cast<const uint4*>(wrow[t] + k) : make_uint4(0, 0, 0, 0);
+        wv[t][s] = ok ? ld16_stream(wrow[t] + k) : make_uint4(0, 0, 0, 0);
       xv[s] = (ok && mvalid) ? *reinterpret_cast<const uint4*>(xrow + k) : make_uint4(0, 0, 0, 0);
     }
     if (NORM) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const int64_t k = kb + s * 8;
+        const int64_t k = kb + s * 32;
         float x[8], w[8];
         unpack8(xv[s], x);
         if (a.norm_w && k < a.K) {
@@ -283,11 +297,11 @@ __global__ __launch_bounds__(kBlock) void linear_scalar_kernel(LinearArgs a) {
 
 template <int M, bool NORM, bool SILU>
 void launch_valu(const LinearArgs& a, hipStream_t s) {
-  constexpr int R = SILU ? 2 : (M == 1 ? 2 : 1);
-  constexpr int U = M <= 2 ? 8 : 4;
+  constexpr int R = SILU ? 2 : (M == 1 ? EZ_GEMV_R1 : 1);
+  constexpr int U = M <= 2 ? EZ_GEMV_U : 4;
   const int64_t waves = SILU ? a.N : (a.N + R - 1) / R;
-  const int64_t blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
-  hipLaunchKernelGGL((gemv_valu_kernel<M, R, U, NORM, SILU>), dim3(blocks), dim3(kBlock), 0, s, a);
+  const int64_t blocks = (waves + kGemvWaves - 1) / kGemvWaves;
+  hipLaunchKernelGGL((gemv_valu_kernel<M, R, U, NORM, SILU>), dim3(blocks), dim3(kGemvBlock), 0, s, a);
 }
 
 template <bool NORM, bool SILU>
@@ -371,5 +385,31 @@ extern "C" int ezops_linear_bf16(const void* X, int64_t ldx, const void* W, void
   a.N = N;
   a.K = K;
   a.epi = ez::kEpiStore;
+  return ez::launch_linear(a, stream);
+}
+
+extern "C" int ezops_linear_stage_bf16(const void* X, int64_t ldx, const void* W, const void* W2, void* Y,
+                                       int64_t ldy, const void* res, int64_t ldr, const void* norm_w, int norm,
+                                       float eps, int epilogue, int64_t M, int64_t N, int64_t K,
+                                       hipStream_t stream) {
+  EZ_REQUIRE(epilogue >= ez::kEpiStore && epilogue <= ez::kEpiStoreF32, "linear_stage: epilogue must be 0..3");
+  EZ_REQUIRE(ldx >= K && ldy >= N && (epilogue != ez::kEpiResid || ldr >= N),
+             "linear_stage: leading dimensions too small");
+  ez::LinearArgs a{};
+  a.X = static_cast<const uint16_t*>(X);
+  a.ldx = ldx;
+  a.W = static_cast<const uint16_t*>(W);
+  a.W2 = static_cast<const uint16_t*>(W2);
+  a.Y = Y;
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.res = static_cast<const uint16_t*>(res);
+  a.ldr = ldr;
+  a.norm = norm != 0;
+  a.norm_w = static_cast<const uint16_t*>(norm_w);
+  a.eps = eps;
+  a.epi = epilogue;
   return ez::launch_linear(a, stream);
 }

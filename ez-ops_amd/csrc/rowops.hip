@@ -226,15 +226,19 @@ __global__ __launch_bounds__(kSumBlock) void sum_kernel(const float* __restrict_
 #pragma unroll
   for (int u = 0; u < kSumUnroll; ++u) s += acc[u];
   s = block_reduce<kSumBlock / kWave, false>(s, red);
-  if (threadIdx.x == 0) partial[blockIdx.x] = s;
+  if (threadIdx.x == 0) st_dev(partial + blockIdx.x, s);
   if (!arrive_last(counter, int(G))) return;
   float t = 0.f;
-  for (int64_t i = threadIdx.x; i < G; i += kSumBlock) t += __builtin_nontemporal_load(partial + i);
+  for (int64_t i = threadIdx.x; i < G; i += kSumBlock) t += ld_dev(partial + i);
   t = block_reduce<kSumBlock / kWave, false>(t, red);
   if (threadIdx.x == 0) Out[0] = t;
 }
 
 // ------------------------------------------------------------ HBM probes
+// Grid-stride STREAM kernels; each thread keeps 4 independent float4
+// accesses in flight per trip.
+constexpr int kProbeUnroll = 4;
+
 __global__ __launch_bounds__(256) void probe_kernel(int kind, float4* __restrict__ a,
                                                     const float4* __restrict__ b,
                                                     const float4* __restrict__ c, int64_t n4, float s) {
@@ -242,6 +246,13 @@ __global__ __launch_bounds__(256) void probe_kernel(int kind, float4* __restrict
   int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (kind == 0) {
     float acc = 0.f;
+    for (; i + (kProbeUnroll - 1) * stride < n4; i += kProbeUnroll * stride) {
+      float4 v[kProbeUnroll];
+#pragma unroll
+      for (int u = 0; u < kProbeUnroll; ++u) v[u] = b[i + u * stride];
+#pragma unroll
+      for (int u = 0; u < kProbeUnroll; ++u) acc += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+    }
     for (; i < n4; i += stride) {
       const float4 v = b[i];
       acc += (v.x + v.y) + (v.z + v.w);
@@ -250,8 +261,27 @@ __global__ __launch_bounds__(256) void probe_kernel(int kind, float4* __restrict
   } else if (kind == 1) {
     for (; i < n4; i += stride) a[i] = make_float4(s, s, s, s);
   } else if (kind == 2) {
+    for (; i + (kProbeUnroll - 1) * stride < n4; i += kProbeUnroll * stride) {
+      float4 v[kProbeUnroll];
+#pragma unroll
+      for (int u = 0; u < kProbeUnroll; ++u) v[u] = b[i + u * stride];
+#pragma unroll
+      for (int u = 0; u < kProbeUnroll; ++u) a[i + u * stride] = v[u];
+    }
     for (; i < n4; i += stride) a[i] = b[i];
   } else {
+    for (; i + (kProbeUnroll - 1) * stride < n4; i += kProbeUnroll * stride) {
+      float4 x[kProbeUnroll], y[kProbeUnroll];
+#pragma unroll
+      for (int u = 0; u < kProbeUnroll; ++u) {
+        x[u] = b[i + u * stride];
+        y[u] = c[i + u * stride];
+      }
+#pragma unroll
+      for (int u = 0; u < kProbeUnroll; ++u)
+        a[i + u * stride] = make_float4(fmaf(s, y[u].x, x[u].x), fmaf(s, y[u].y, x[u].y), fmaf(s, y[u].z, x[u].z),
+                                        fmaf(s, y[u].w, x[u].w));
+    }
     for (; i < n4; i += stride) {
       const float4 x = b[i], y = c[i];
       a[i] = make_float4(fmaf(s, y.x, x.x), fmaf(s, y.y, x.y), fmaf(s, y.z, x.z), fmaf(s, y.w, x.w));
@@ -381,7 +411,7 @@ extern "C" int ezops_hbm_probe(int kind, float* a, const float* b, const float* 
   EZ_REQUIRE(kind >= 0 && kind <= 3, "hbm_probe: kind must be 0..3");
   EZ_REQUIRE(a && (kind == 1 || b) && (kind != 3 || c), "hbm_probe: null pointer");
   EZ_REQUIRE(n >= 4 && n % 4 == 0, "hbm_probe: n must be a positive multiple of 4");
-  const int64_t blocks = int64_t(num_cus()) * 8;
+  const int64_t blocks = int64_t(num_cus()) * 16;
   hipLaunchKernelGGL(probe_kernel, dim3(unsigned(blocks)), dim3(256), 0, s, kind, reinterpret_cast<float4*>(a),
                      reinterpret_cast<const float4*>(b), reinterpret_cast<const float4*>(c), n / 4, sc);
   return launch_status("hbm_probe");

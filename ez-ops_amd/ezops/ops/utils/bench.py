@@ -9,7 +9,9 @@ MI355X difference: the reference sizes its flush buffer to
 ``L2_cache_size``.  Here L2 is 4 MB per XCD but the 256 MB Infinity Cache
 (MALL) sits behind it, so a weight of a few hundred MB would stay resident
 and the measured GB/s would be inflated.  The flush writes 1 GiB, four times
-the MALL.
+the MALL.  The flush *reads* the buffer (a sum kernel): a write flush would
+leave the MALL full of dirty lines whose write-back then competes with the
+kernel being timed.
 """
 
 from __future__ import annotations
@@ -24,11 +26,16 @@ _flush_buf: Optional[torch.Tensor] = None
 
 
 def flush_cache() -> None:
-    """Overwrite 1 GiB on the current stream, evicting L2 and MALL."""
+    """Read 1 GiB on the current stream, evicting L2 and MALL with clean lines."""
     global _flush_buf
+    from ... import _hip
+
     if _flush_buf is None:
-        _flush_buf = torch.empty(FLUSH_BYTES // 4, dtype=torch.int32, device="cuda")
-    _flush_buf.zero_()
+        _flush_buf = torch.zeros(FLUSH_BYTES // 4 + 4, dtype=torch.float32, device="cuda")
+    n = FLUSH_BYTES // 4
+    # kind 0 = read probe; the 4 extra floats receive its (never taken) store
+    _hip.call("ezops_hbm_probe", 0, _flush_buf[n:].data_ptr(), _flush_buf.data_ptr(), None, n, 0.0,
+              _hip.stream())
 
 
 def bench_kernel(

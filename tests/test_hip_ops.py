@@ -135,6 +135,32 @@ def test_attn_decode(B, H, Hkv, S, D, ragged):
     assert torch.equal(out, out2)
 
 
+@pytest.mark.parametrize("B,S", [(1, 16384), (8, 4096)])
+def test_attn_decode_consecutive_calls_fresh_partials(B, S):
+    """Split partials are handed between blocks through device-coherent
+    accesses; consecutive calls with new inputs must never see the previous
+    call's partials."""
+    op = AttnDecodeOp(B, 32, S, 128, backend="hip", num_kv_heads=8)
+    torch.manual_seed(11)
+    Q, K, V = op.gen_data()
+    lens = torch.randint(S // 2, S + 1, (B,), dtype=torch.int32).to(DEV)
+    nK, nV = n(K), n(V)
+    for it in range(4):
+        Q = torch.randn_like(Q, dtype=torch.float32).mul_(1 + it).to(torch.bfloat16)
+        out = op(Q, K, V, lens)
+        ref = oracle.attn_decode(n(Q)[:, :, 0], nK, nV, n(lens).astype(np.int64))
+        np.testing.assert_allclose(n(out)[:, :, 0], ref, **BF_TOL)
+
+
+def test_reduce_consecutive_calls():
+    op = ReduceOp(1 << 22, backend="hip")
+    Out = torch.empty(1, device=DEV)
+    for it in range(4):
+        A = (torch.rand(1 << 22, device=DEV) * 2 - 1) * (it + 1)
+        op(A, Out)
+        assert abs(Out.item() - oracle.reduce_sum(n(A))[0]) <= 1e-7 * (1 << 22)
+
+
 def test_attn_decode_stream_and_graph():
     torch.manual_seed(5)
     op = AttnDecodeOp(2, 32, 2048, 128, backend="hip", num_kv_heads=8)
