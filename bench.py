@@ -5,10 +5,10 @@ bandwidth, and microseconds per Qwen3-8B dense decode layer at batch 1
 (config L: hidden 4096, 32/8 heads x 128, intermediate 12288, RMSNorm eps
 1e-6 with weights, RoPE theta 1e6, KV length ~ U[1024, 16384], seed 4).
 
-One "step" = one decode-layer forward (6 kernels, replayed from a HIP graph)
-with every input already in HBM.  Between steps a 1 GiB write evicts L2 and
+One "step" = one decode-layer forward (5 kernels, replayed from a HIP graph)
+with every input already in HBM.  Between steps a 1 GiB read evicts L2 and
 the 256 MB MALL (outside the timed events), so each step streams its
-~421 MB from HBM.  The per-op table covers the other BASELINE configs.
+~424 MB from HBM.  The per-op table covers the other BASELINE configs.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-ops] [--no-cpu]
 Prints ONE JSON line.
@@ -259,18 +259,27 @@ def main() -> int:
     us = ms * 1e3
     gbps = nbytes / (ms * 1e-3) / 1e9
 
-    # dominant kernel: the RMSNorm + gate/up + SwiGLU stage (201 MB of the ~421 MB)
+    # Dominant kernel: the RMSNorm + gate/up + SwiGLU stage (201 MB of the
+    # ~424 MB).  Its per-launch duration is measured over back-to-back
+    # launches that rotate through 3 weight copies (604 MB > 256 MB MALL), so
+    # every launch streams from HBM and the graph-launch latency is amortised.
     HS, IS = 4096, 12288
-    x2 = data[0]
+    x2, post_w = data[0], data[10]
+    copies = [data[5]] + [data[5].clone() for _ in range(2)]
     h = torch.empty(B, IS, dtype=torch.bfloat16, device="cuda")
-    Wgu, post_w = data[5], data[10]
-    def gate_up():  # launched on the current (capturing) stream
-        _hip.call("ezops_linear_stage_bf16", x2.data_ptr(), HS, Wgu.data_ptr(), Wgu[IS:].data_ptr(), h.data_ptr(),
-                  IS, None, 0, post_w.data_ptr(), 1, 1e-6, 2, B, IS, HS, _hip.stream())
+    n_launch = 12
 
-    gu_ms = statistics.mean(time_graph(gate_up, args.steps, args.warmup, flush_cache))
+    def gate_up_chain():  # launched on the current (capturing) stream
+        for i in range(n_launch):
+            W = copies[i % len(copies)]
+            _hip.call("ezops_linear_stage_bf16", x2.data_ptr(), HS, W.data_ptr(), W[IS:].data_ptr(), h.data_ptr(),
+                      IS, None, 0, post_w.data_ptr(), 1, 1e-6, 2, B, IS, HS, _hip.stream())
+
+    gu_ms = statistics.mean(time_graph(gate_up_chain, max(5, args.steps // 3), 2, flush_cache)) / n_launch
     gu_bytes = 2 * IS * HS * 2 + B * HS * 2 + HS * 2 + B * IS * 2
     gu_gbps = gu_bytes / (gu_ms * 1e-3) / 1e9
+    del copies
+    torch.cuda.empty_cache()
 
     result = {
         "metric": METRIC,
@@ -297,7 +306,9 @@ def main() -> int:
         "roofline": {"kernel": "gemv_valu_kernel (RMSNorm + gate/up + SwiGLU stage)", "bound": "hbm",
                      "achieved": round(gu_gbps, 1), "peak": SPEC_HBM_GBPS, "unit": "GB/s",
                      "frac": round(gu_gbps / SPEC_HBM_GBPS, 4), "frac_of_measured_peak": round(gu_gbps / peak, 4),
-                     "us": round(gu_ms * 1e3, 2), "algorithmic_bytes": gu_bytes, "traffic": None},
+                     "us": round(gu_ms * 1e3, 2), "algorithmic_bytes": gu_bytes, "traffic": None,
+                     "timing": f"HIP events over {n_launch} back-to-back launches per graph replay, "
+                               "3 rotating weight copies"},
     }
 
     if not args.no_cpu:

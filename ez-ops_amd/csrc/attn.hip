@@ -1,37 +1,41 @@
 // Split-KV GQA decode attention for one query token per sequence.
 //
-// Work unit = (sequence b, kv head, split).  One block of 4 waves owns a
+// Work unit = (sequence b, kv head, split).  One block of W waves owns a
 // contiguous chunk of KV positions of one (b, kv head); its G = H / Hkv query
 // heads share every K/V byte it loads, so K/V cross HBM once per GQA group.
-// Each wave walks 64-position tiles:
+// Each wave walks 32-position tiles:
 //   * scores S[h, p] = q_h . k_p on MFMA (v_mfma_f32_16x16x32_bf16): A = the
 //     G query rows (zero-padded to 16), B = 16 positions of K per sub-tile;
-//     every lane loads 16-byte pieces of K rows straight into the B operand.
-//   * online softmax in the exp2 domain (scale * log2 e folded into S), with
-//     the running max kept wave-uniform.
-//   * O += P . V on VALU: the 64 V rows are read with fully coalesced 16-byte
-//     loads (one wave instruction covers 1 KiB of consecutive rows); P goes
-//     through a 1 KiB LDS slice per wave and is read back as broadcasts.
-// The 4 waves merge their (max, sum, O) through LDS; with more than one
-// split, the block stores an fp32 partial and the last block of the unit
-// (device-scope arrival counter) merges all splits and writes bf16 output.
+//     lanes load 16-byte pieces of K rows straight into the B operand.
+//   * online softmax in the exp2 domain (scale * log2 e folded into S), the
+//     running max kept wave-uniform, row maxima by DPP.
+//   * O += P . V on VALU: V rows are read with fully coalesced 16-byte loads
+//     (one wave instruction covers 1 KiB of consecutive rows); P goes through
+//     a small LDS slice per wave and is read back as broadcasts.
+//   * the next tile's K is requested right after the MFMAs and the next V
+//     right after the P.V update, so loads overlap the softmax / FMA work.
+// The W waves merge their (max, sum, O) through LDS.  With more than one
+// split, the block hands an fp32 partial to the last block of its unit
+// (device-scope arrival counter, sc1 stores/loads, no cache flushes), which
+// merges all splits with every partial load in flight at once.
+//
+// Few units (small batch) use 8-wave blocks and at most 32 splits; many
+// units use 4-wave blocks.
 #include "common.h"
 #include "internal.h"
 #include "status.h"
 #include "../../include/ezops_hip.h"
 
-namespace ez {
-namespace {
-
-constexpr int kAttnBlock = 256;
-constexpr int kAttnWaves = 4;
 #ifndef EZ_ATTN_TILE
 #define EZ_ATTN_TILE 32
 #endif
+
+namespace ez {
+namespace {
+
 constexpr int kTile = EZ_ATTN_TILE;  // positions per wave iteration
-constexpr int kMinChunk = kTile * kAttnWaves;
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kMaxSplits = 64;  // one wave reads all split statistics in the merge
+constexpr int kMaxSplits = 32;       // split partials a merge thread loads at once
 
 int num_cus() {
   static int cus = 0;
@@ -45,21 +49,27 @@ int num_cus() {
 }
 
 struct SplitPlan {
+  int waves;
   int64_t nsplit, chunk;
 };
 
-SplitPlan plan_splits(int64_t B, int64_t Hkv, int64_t S) {
+SplitPlan plan_splits(int64_t B, int64_t Hkv, int64_t S, int64_t G) {
   const int64_t units = B * Hkv;
-  const int64_t target = int64_t(num_cus()) * 8;
+  const int64_t cus = num_cus();
+  // 8-wave blocks for few units; group 8 keeps 4 waves (its accumulators need
+  // the register budget of one wave per SIMD).
+  const int waves = (units * 4 <= cus && G <= 4) ? 8 : 4;
+  const int64_t target = waves == 8 ? 2 * cus : 8 * cus;  // blocks in flight
   int64_t ns = (target + units - 1) / units;
-  const int64_t max_ns = (S + kMinChunk - 1) / kMinChunk;
+  const int64_t min_chunk = int64_t(waves) * kTile;
+  const int64_t max_ns = (S + min_chunk - 1) / min_chunk;
   if (ns > max_ns) ns = max_ns;
   if (ns > kMaxSplits) ns = kMaxSplits;
   if (ns < 1) ns = 1;
   int64_t chunk = (S + ns - 1) / ns;
   chunk = (chunk + kTile - 1) / kTile * kTile;
   ns = (S + chunk - 1) / chunk;
-  return {ns, chunk};
+  return {waves, ns, chunk};
 }
 
 struct AttnWs {
@@ -101,9 +111,48 @@ __device__ __forceinline__ void load_v_tile(const uint16_t* Vb, int64_t t0, int6
   }
 }
 
-template <int D, int G>
-__global__ __launch_bounds__(kAttnBlock) void attn_split_kernel(AttnArgs a, int64_t nsplit,
-                                                               int64_t chunk, AttnWs ws) {
+// Qwen3 per-head RMSNorm (fp32 statistics, weight) + half-split RoPE of one
+// head held in bf16 at `src`, rounded once to bf16 into `dst` (LDS or global).
+// One wave; lane l owns the pairs (i, i + D/2), i = l, l + 64, ...  Operation
+// order follows the reference (ezops/ops/fused_qk_norm_rope.py:138-147).
+template <int D>
+__device__ __forceinline__ void norm_rope_head(const uint16_t* src, const uint16_t* w, const uint16_t* crow,
+                                               const uint16_t* srow, float eps, uint16_t* dst, int lane) {
+  constexpr int HALF = D / 2;
+  constexpr int NP = (HALF + kWave - 1) / kWave;
+  float x1[NP], x2[NP];
+  float ss = 0.f;
+#pragma unroll
+  for (int t = 0; t < NP; ++t) {
+    const int i = lane + t * kWave;
+    x1[t] = i < HALF ? bf2f(src[i]) : 0.f;
+    x2[t] = i < HALF ? bf2f(src[i + HALF]) : 0.f;
+    ss += x1[t] * x1[t] + x2[t] * x2[t];
+  }
+  const float r = rsqrtf(wave_sum(ss) / float(D) + eps);
+#pragma unroll
+  for (int t = 0; t < NP; ++t) {
+    const int i = lane + t * kWave;
+    if (i >= HALF) break;
+    float y1 = __fmul_rn(x1[t], r), y2 = __fmul_rn(x2[t], r);
+    if (w) {
+      y1 = __fmul_rn(y1, bf2f(w[i]));
+      y2 = __fmul_rn(y2, bf2f(w[i + HALF]));
+    }
+    float o1 = y1, o2 = y2;
+    if (crow) {
+      o1 = __fadd_rn(__fmul_rn(y1, bf2f(crow[i])), __fmul_rn(-y2, bf2f(srow[i])));
+      o2 = __fadd_rn(__fmul_rn(y2, bf2f(crow[i + HALF])), __fmul_rn(y1, bf2f(srow[i + HALF])));
+    }
+    dst[i] = f2bf(o1);
+    dst[i + HALF] = f2bf(o2);
+  }
+}
+
+template <int D, int G, int W, bool LAYER>
+__global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int64_t nsplit, int64_t chunk,
+                                                               AttnWs ws) {
+  constexpr int NT = W * kWave;      // threads per block
   constexpr int NS = D / 32;         // MFMA k-steps per 16-position sub-tile
   constexpr int CPR = D / 8;         // 16-byte chunks per K/V row
   constexpr int RPI = kWave / CPR;   // rows covered by one wave-wide V load
@@ -112,10 +161,11 @@ __global__ __launch_bounds__(kAttnBlock) void attn_split_kernel(AttnArgs a, int6
   constexpr int GP = G <= 4 ? 4 : 8; // P row stride in LDS (float4 reads)
   static_assert(G <= 8, "group size");
 
-  __shared__ __align__(16) float Ps[kAttnWaves][kTile][GP];
-  __shared__ __align__(16) float Os[kAttnWaves][G][D];
-  __shared__ float Ms[kAttnWaves][G], Ls[kAttnWaves][G];
+  __shared__ __align__(16) float Ps[W][kTile][GP];
+  __shared__ __align__(16) float Os[W][G][D];
+  __shared__ float Ms[W][G], Ls[W][G];
   __shared__ float Wt[G][kMaxSplits];
+  __shared__ __align__(16) uint16_t Qs[LAYER ? G : 1][D];
 
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
@@ -134,20 +184,52 @@ __global__ __launch_bounds__(kAttnBlock) void attn_split_kernel(AttnArgs a, int6
   const float sl2 = a.scale * kLog2e;
   const int dc = lane % CPR, rs = lane / CPR;
 
+  // The block whose chunk holds the decoded token writes its k/v first and
+  // only then loads K/V tiles; every other block starts its loads at once.
+  const int64_t pos = L - 1;
+  const bool owner = LAYER && pos >= p_begin && pos < p_end;
   int64_t t0 = p_begin + int64_t(wave) * kTile;
   uint4 kf[NSUB][NS], vf[NPV];
-  if (t0 < p_end) {
+  if (!owner && t0 < p_end) {
     load_k_tile<D, NSUB>(Kb, t0, last, li, lg, kf);
     load_v_tile<D, NPV>(Vb, t0, last, dc, rs, vf);
   }
 
-  // Q operand: lane (li, lg) holds Q[h0 + li][s*32 + lg*8 .. +8] for step s.
   bf16x8_t qf[NS];
+  if constexpr (LAYER) {
+    if (L > 0) {
+      const uint16_t* row = a.qkv + b * a.qkv_bs;
+      const uint16_t* crow = a.cos ? a.cos + pos * D : nullptr;
+      const uint16_t* srow = a.sin ? a.sin + pos * D : nullptr;
+      for (int h = wave; h < G; h += W)
+        norm_rope_head<D>(row + (h0 + h) * D, a.qw, crow, srow, a.eps, &Qs[h][0], lane);
+      if (owner && wave == W - 1) {
+        const int64_t kofs = a.H * D + kvh * D, vofs = (a.H + a.Hkv) * D + kvh * D;
+        uint16_t* kdst = const_cast<uint16_t*>(Kb) + pos * D;
+        uint16_t* vdst = const_cast<uint16_t*>(Vb) + pos * D;
+        norm_rope_head<D>(row + kofs, a.kw, crow, srow, a.eps, kdst, lane);
+        for (int i = lane; i < D; i += kWave) vdst[i] = row[vofs + i];
+      }
+    }
+    __syncthreads();  // Qs complete; the cache slot written by this block is visible to it
+    if (owner && t0 < p_end) {
+      load_k_tile<D, NSUB>(Kb, t0, last, li, lg, kf);
+      load_v_tile<D, NPV>(Vb, t0, last, dc, rs, vf);
+    }
 #pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (li < G) v = *reinterpret_cast<const uint4*>(a.Q + ((b * a.H + h0 + li) * D) + 32 * s + lg * 8);
-    qf[s] = as_bf16x8(v);
+    for (int s = 0; s < NS; ++s) {
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (li < G) v = *reinterpret_cast<const uint4*>(&Qs[li][32 * s + lg * 8]);
+      qf[s] = as_bf16x8(v);
+    }
+  } else {
+    // Q operand: lane (li, lg) holds Q[h0 + li][s*32 + lg*8 .. +8] for step s.
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (li < G) v = *reinterpret_cast<const uint4*>(a.Q + ((b * a.H + h0 + li) * D) + 32 * s + lg * 8);
+      qf[s] = as_bf16x8(v);
+    }
   }
 
   float m_run[G], l_acc[G], o[G][8];
@@ -159,8 +241,8 @@ __global__ __launch_bounds__(kAttnBlock) void attn_split_kernel(AttnArgs a, int6
     for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
   }
 
-  for (; t0 < p_end; t0 += int64_t(kAttnWaves) * kTile) {
-    const int64_t tn = t0 + int64_t(kAttnWaves) * kTile;
+  for (; t0 < p_end; t0 += int64_t(W) * kTile) {
+    const int64_t tn = t0 + int64_t(W) * kTile;
     // ---- scores: acc[u][j] = S[head 4*lg + j][pos t0 + 16u + li]
     f32x4_t acc[NSUB];
 #pragma unroll
@@ -264,15 +346,15 @@ __global__ __launch_bounds__(kAttnBlock) void attn_split_kernel(AttnArgs a, int6
   }
   __syncthreads();
 
-  // ---- merge the 4 waves: thread handles (h, d) pairs
-  for (int idx = threadIdx.x; idx < G * D; idx += kAttnBlock) {
+  // ---- merge the W waves: thread handles (h, d) pairs
+  for (int idx = threadIdx.x; idx < G * D; idx += NT) {
     const int h = idx / D, d = idx % D;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, Ms[w][h]);
+    for (int w = 0; w < W; ++w) M = fmaxf(M, Ms[w][h]);
     float ov = 0.f, lv = 0.f;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) {
+    for (int w = 0; w < W; ++w) {
       const float f = (Ms[w][h] == -INFINITY) ? 0.f : exp2f(Ms[w][h] - M);
       ov = fmaf(f, Os[w][h][d], ov);
       lv = fmaf(f, Ls[w][h], lv);
@@ -293,8 +375,8 @@ __global__ __launch_bounds__(kAttnBlock) void attn_split_kernel(AttnArgs a, int6
 
   // ---- last block of the unit merges the splits.
   // (1) per head: one wave reads the nsplit (max, sum) pairs at once and
-  //     turns them into normalised weights w_s = 2^(m_s - M) / sum_s' ...
-  for (int h = wave; h < G; h += kAttnWaves) {
+  //     turns them into normalised weights w_s = 2^(m_s - M) / sum.
+  for (int h = wave; h < G; h += W) {
     const int64_t hq = b * a.H + h0 + h;
     const float* ml = ws.ml + hq * nsplit * 2;
     const bool ok = lane < nsplit;
@@ -306,35 +388,47 @@ __global__ __launch_bounds__(kAttnBlock) void attn_split_kernel(AttnArgs a, int6
     if (ok) Wt[h][lane] = tot > 0.f ? f / tot : 0.f;
   }
   __syncthreads();
-  // (2) thread per (h, d): weighted sum of the split partials, loads issued
-  //     eight at a time.
-  for (int idx = threadIdx.x; idx < G * D; idx += kAttnBlock) {
+  // (2) thread per (h, d): weighted sum of the split partials; all nsplit
+  //     loads of a thread are issued before the first is used.
+  for (int idx = threadIdx.x; idx < G * D; idx += NT) {
     const int h = idx / D, d = idx % D;
     const int64_t hq = b * a.H + h0 + h;
     const float* op = ws.opart + hq * nsplit * D + d;
-    float acc8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    int64_t s0 = 0;
-    for (; s0 + 8 <= nsplit; s0 += 8) {
-      float v8[8];
+    constexpr int CB = G > 4 ? kMaxSplits / 2 : kMaxSplits;  // loads in flight (register budget)
+    float acc = 0.f;
+    for (int s0 = 0; s0 < nsplit; s0 += CB) {
+      float v[CB];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v8[e] = ld_dev(op + (s0 + e) * D);
+      for (int e = 0; e < CB; ++e) v[e] = s0 + e < nsplit ? ld_dev(op + (s0 + e) * D) : 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc8[e] = fmaf(Wt[h][s0 + e], v8[e], acc8[e]);
+      for (int e = 0; e < CB; ++e)
+        if (s0 + e < nsplit) acc = fmaf(Wt[h][s0 + e], v[e], acc);
     }
-    for (; s0 < nsplit; ++s0) acc8[0] = fmaf(Wt[h][s0], ld_dev(op + s0 * D), acc8[0]);
-    const float r = ((acc8[0] + acc8[1]) + (acc8[2] + acc8[3])) + ((acc8[4] + acc8[5]) + (acc8[6] + acc8[7]));
-    a.Out[hq * D + d] = f2bf(r);
+    a.Out[hq * D + d] = f2bf(acc);
   }
 }
 
-template <int D>
-void launch_d(const AttnArgs& a, const SplitPlan& pl, const AttnWs& ws, int64_t G, hipStream_t s) {
-  const dim3 grid{unsigned(a.B * a.Hkv * pl.nsplit), 1, 1}, block{kAttnBlock, 1, 1};
+template <int D, int W, bool LAYER>
+void launch_dw(const AttnArgs& a, const SplitPlan& pl, const AttnWs& ws, int64_t G, hipStream_t s) {
+  const dim3 grid{unsigned(a.B * a.Hkv * pl.nsplit), 1, 1}, block{unsigned(W * kWave), 1, 1};
   switch (G) {
-    case 1: hipLaunchKernelGGL((attn_split_kernel<D, 1>), grid, block, 0, s, a, pl.nsplit, pl.chunk, ws); break;
-    case 2: hipLaunchKernelGGL((attn_split_kernel<D, 2>), grid, block, 0, s, a, pl.nsplit, pl.chunk, ws); break;
-    case 4: hipLaunchKernelGGL((attn_split_kernel<D, 4>), grid, block, 0, s, a, pl.nsplit, pl.chunk, ws); break;
-    default: hipLaunchKernelGGL((attn_split_kernel<D, 8>), grid, block, 0, s, a, pl.nsplit, pl.chunk, ws); break;
+    case 1: hipLaunchKernelGGL((attn_split_kernel<D, 1, W, LAYER>), grid, block, 0, s, a, pl.nsplit, pl.chunk, ws); break;
+    case 2: hipLaunchKernelGGL((attn_split_kernel<D, 2, W, LAYER>), grid, block, 0, s, a, pl.nsplit, pl.chunk, ws); break;
+    case 4: hipLaunchKernelGGL((attn_split_kernel<D, 4, W, LAYER>), grid, block, 0, s, a, pl.nsplit, pl.chunk, ws); break;
+    default: break;  // group 8 launches from launch_d
+  }
+}
+
+template <int D, bool LAYER>
+void launch_d(const AttnArgs& a, const SplitPlan& pl, const AttnWs& ws, int64_t G, hipStream_t s) {
+  const dim3 block{unsigned(pl.waves * kWave), 1, 1};
+  const dim3 grid{unsigned(a.B * a.Hkv * pl.nsplit), 1, 1};
+  if (G == 8) {
+    hipLaunchKernelGGL((attn_split_kernel<D, 8, 4, LAYER>), grid, block, 0, s, a, pl.nsplit, pl.chunk, ws);
+  } else if (pl.waves == 8) {
+    launch_dw<D, 8, LAYER>(a, pl, ws, G, s);
+  } else {
+    launch_dw<D, 4, LAYER>(a, pl, ws, G, s);
   }
 }
 
@@ -342,19 +436,21 @@ void launch_d(const AttnArgs& a, const SplitPlan& pl, const AttnWs& ws, int64_t 
 
 size_t attn_workspace_size(int64_t B, int64_t H, int64_t Hkv, int64_t S, int64_t D) {
   if (B < 1 || H < 1 || Hkv < 1 || S < 1 || D < 1) return 0;
-  const SplitPlan pl = plan_splits(B, Hkv, S);
+  const SplitPlan pl = plan_splits(B, Hkv, S, H / Hkv);
   return align256(size_t(B * H * pl.nsplit * D) * 4) + align256(size_t(B * H * pl.nsplit * 2) * 4) +
          align256(size_t(B * Hkv) * 4);
 }
 
 int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
-  EZ_REQUIRE(a.Q && a.K && a.V && a.Out, "attn_decode: null pointer");
+  const bool layer = a.Q == nullptr;
+  EZ_REQUIRE(a.K && a.V && a.Out && (!layer || a.qkv), "attn_decode: null pointer");
   EZ_REQUIRE(a.B >= 1 && a.H >= 1 && a.Hkv >= 1 && a.S >= 1, "attn_decode: bad shape");
   EZ_REQUIRE(a.H % a.Hkv == 0, "attn_decode: num_heads must be divisible by num_kv_heads");
   const int64_t G = a.H / a.Hkv;
   EZ_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "attn_decode: group size %lld not in {1,2,4,8}", (long long)G);
   EZ_REQUIRE(a.D == 64 || a.D == 128, "attn_decode: head_dim must be 64 or 128");
-  const SplitPlan pl = plan_splits(a.B, a.Hkv, a.S);
+  EZ_REQUIRE((a.cos == nullptr) == (a.sin == nullptr), "attn_decode: cos and sin go together");
+  const SplitPlan pl = plan_splits(a.B, a.Hkv, a.S, G);
   AttnWs w{};
   if (pl.nsplit > 1) {
     EZ_REQUIRE(ws && ws_bytes >= attn_workspace_size(a.B, a.H, a.Hkv, a.S, a.D),
@@ -369,8 +465,13 @@ int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
   }
   AttnArgs aa = a;
   if (aa.scale <= 0.f) aa.scale = 1.0f / sqrtf(float(a.D));
-  if (a.D == 64) launch_d<64>(aa, pl, w, G, s);
-  else launch_d<128>(aa, pl, w, G, s);
+  if (layer) {
+    if (a.D == 64) launch_d<64, true>(aa, pl, w, G, s);
+    else launch_d<128, true>(aa, pl, w, G, s);
+  } else {
+    if (a.D == 64) launch_d<64, false>(aa, pl, w, G, s);
+    else launch_d<128, false>(aa, pl, w, G, s);
+  }
   return launch_status("attn_decode");
 }
 
@@ -383,6 +484,7 @@ extern "C" size_t ezops_attn_decode_workspace_size(int64_t B, int64_t H, int64_t
 extern "C" int ezops_attn_decode_bf16(const void* Q, const void* K, const void* V, void* Out, int64_t B,
                                       int64_t H, int64_t Hkv, int64_t S, int64_t D, const int32_t* kv_lens,
                                       float scale, void* ws, size_t ws_bytes, hipStream_t stream) {
+  EZ_REQUIRE(Q, "attn_decode: null pointer");
   ez::AttnArgs a{};
   a.Q = static_cast<const uint16_t*>(Q);
   a.K = static_cast<const uint16_t*>(K);

@@ -6,8 +6,8 @@
 //                                                       SwiGLU epilogue)
 //                  out = x2 + h.Wd^T                 (linear, residual epilogue)
 //   layer:         qkv = n(hidden).Wqkv^T            (linear, RMSNorm prologue)
-//                  q, k-slot, v-slot = qk_norm_rope(qkv)
-//                  attn = gqa_decode(q, K_cache, V_cache)
+//                  attn = gqa_decode(norm_rope(q), K/V cache + this token's
+//                         norm_rope(k), v), one kernel (attn.hip)
 //                  out = o_proj + FFN(attn, hidden)
 #include <hip/hip_runtime.h>
 
@@ -87,7 +87,6 @@ extern "C" size_t ezops_qwen3_layer_workspace_size(const ezops_qwen3_layer* p) {
   if (!p) return 0;
   const int64_t QR = p->H * p->D, KVR = p->Hkv * p->D;
   return align256(size_t(p->B * (QR + 2 * KVR)) * 2)   // qkv
-         + align256(size_t(p->B * QR) * 2)              // normed/rotated q
          + align256(size_t(p->B * QR) * 2)              // attention output
          + align256(attn_workspace_size(p->B, p->H, p->Hkv, p->S, p->D)) + ffn_ws(p->B, p->HS, p->IS);
 }
@@ -105,7 +104,6 @@ extern "C" int ezops_qwen3_dense_decode_bf16(const ezops_qwen3_layer* p, void* w
   const int64_t QR = p->H * p->D, KVR = p->Hkv * p->D, QKV = QR + 2 * KVR;
   Carve c{static_cast<char*>(ws)};
   uint16_t* qkv = c.take<uint16_t>(size_t(p->B * QKV) * 2);
-  uint16_t* qn = c.take<uint16_t>(size_t(p->B * QR) * 2);
   uint16_t* att = c.take<uint16_t>(size_t(p->B * QR) * 2);
   char* attn_ws = c.take<char>(attn_workspace_size(p->B, p->H, p->Hkv, p->S, p->D));
   char* ffn = c.p;
@@ -118,31 +116,22 @@ extern "C" int ezops_qwen3_dense_decode_bf16(const ezops_qwen3_layer* p, void* w
   int rc = launch_linear(l, s);
   if (rc) return rc;
 
-  QkRopeArgs r{};
-  r.q = qkv; r.q_bs = QKV;
-  r.k = qkv + QR; r.k_bs = QKV;
-  r.v = qkv + QR + KVR; r.v_bs = QKV;
-  r.qw = static_cast<const uint16_t*>(p->q_norm_w);
-  r.kw = static_cast<const uint16_t*>(p->k_norm_w);
-  r.cos = static_cast<const uint16_t*>(p->cos);
-  r.sin = static_cast<const uint16_t*>(p->sin);
-  r.Kc = static_cast<uint16_t*>(p->K_cache);
-  r.Vc = static_cast<uint16_t*>(p->V_cache);
-  r.q_out = qn; r.k_out = nullptr;
-  r.B = p->B; r.H = p->H; r.Hkv = p->Hkv; r.D = p->D; r.S = p->S;
-  r.position = p->S - 1; r.positions = p->kv_lens; r.pos_offset = p->kv_lens ? -1 : 0;
-  r.eps = p->eps;
-  rc = launch_qk_norm_rope(r, s);
-  if (rc) return rc;
-
+  // q/k RMSNorm + RoPE and the K/V-cache write of the decoded token run in
+  // the attention kernel's prologue (attn.hip), reading the bf16 QKV row.
   AttnArgs a{};
-  a.Q = qn;
+  a.Q = nullptr;
   a.K = static_cast<const uint16_t*>(p->K_cache);
   a.V = static_cast<const uint16_t*>(p->V_cache);
   a.Out = att;
   a.B = p->B; a.H = p->H; a.Hkv = p->Hkv; a.S = p->S; a.D = p->D;
   a.kv_lens = p->kv_lens;
   a.scale = 0.f;
+  a.qkv = qkv; a.qkv_bs = QKV;
+  a.qw = static_cast<const uint16_t*>(p->q_norm_w);
+  a.kw = static_cast<const uint16_t*>(p->k_norm_w);
+  a.cos = static_cast<const uint16_t*>(p->cos);
+  a.sin = static_cast<const uint16_t*>(p->sin);
+  a.eps = p->eps;
   rc = launch_attn(a, attn_ws, attn_workspace_size(p->B, p->H, p->Hkv, p->S, p->D), s);
   if (rc) return rc;
 

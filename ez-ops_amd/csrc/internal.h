@@ -46,12 +46,21 @@ struct QkRopeArgs {
 int launch_qk_norm_rope(const QkRopeArgs& a, hipStream_t s);
 
 struct AttnArgs {
-  const uint16_t* Q;  // [B, H, D]
+  const uint16_t* Q;  // [B, H, D]; NULL selects the fused layer prologue below
   const uint16_t* K; const uint16_t* V;  // [B, Hkv, S, D]
   uint16_t* Out;      // [B, H, D]
   int64_t B, H, Hkv, S, D;
   const int32_t* kv_lens;
   float scale;
+  // Fused layer prologue (Q == NULL): q/k/v of the decoded token come from
+  // the bf16 QKV projection (row b at qkv + b*qkv_bs, columns [q | k | v]);
+  // q and k get the per-head RMSNorm (weights qw/kw, NULL = unit) and RoPE
+  // (cos/sin rows at the token position, NULL = none), and the block whose
+  // split holds the token position writes k and v into the cache slot.
+  const uint16_t* qkv; int64_t qkv_bs;
+  const uint16_t* qw; const uint16_t* kw;
+  const uint16_t* cos; const uint16_t* sin;
+  float eps;
 };
 size_t attn_workspace_size(int64_t B, int64_t H, int64_t Hkv, int64_t S, int64_t D);
 int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s);
