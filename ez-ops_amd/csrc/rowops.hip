@@ -235,56 +235,53 @@ __global__ __launch_bounds__(kSumBlock) void sum_kernel(const float* __restrict_
 }
 
 // ------------------------------------------------------------ HBM probes
-// Grid-stride STREAM kernels; each thread keeps 4 independent float4
-// accesses in flight per trip.
-constexpr int kProbeUnroll = 4;
+// STREAM kernels, one instantiation per kind (measured shapes):
+//   read:            grid-stride, 8 float4 loads in flight per thread;
+//   write/copy/triad: each block streams one contiguous range (DRAM page
+//                    locality, ~20% faster than grid-striding on MI355X),
+//                    8 float4 per thread per trip, non-temporal stores.
+constexpr int kProbeUnroll = 8;
+typedef float f32x4v_t __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(256) void probe_kernel(int kind, float4* __restrict__ a,
-                                                    const float4* __restrict__ b,
-                                                    const float4* __restrict__ c, int64_t n4, float s) {
-  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
-  int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (kind == 0) {
-    float acc = 0.f;
-    for (; i + (kProbeUnroll - 1) * stride < n4; i += kProbeUnroll * stride) {
-      float4 v[kProbeUnroll];
+__global__ __launch_bounds__(256) void probe_read_kernel(const f32x4v_t* __restrict__ b, int64_t n4,
+                                                         f32x4v_t* __restrict__ sink) {
+  const int64_t stride = int64_t(gridDim.x) * 256;
+  int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  f32x4v_t acc = {0.f, 0.f, 0.f, 0.f};
+  for (; i + (kProbeUnroll - 1) * stride < n4; i += kProbeUnroll * stride) {
+    f32x4v_t x[kProbeUnroll];
 #pragma unroll
-      for (int u = 0; u < kProbeUnroll; ++u) v[u] = b[i + u * stride];
+    for (int u = 0; u < kProbeUnroll; ++u) x[u] = b[i + u * stride];
 #pragma unroll
-      for (int u = 0; u < kProbeUnroll; ++u) acc += (v[u].x + v[u].y) + (v[u].z + v[u].w);
-    }
-    for (; i < n4; i += stride) {
-      const float4 v = b[i];
-      acc += (v.x + v.y) + (v.z + v.w);
-    }
-    if (acc == 1234.5f) a[0].x = acc;  // keeps the loads alive; practically never stores
-  } else if (kind == 1) {
-    for (; i < n4; i += stride) a[i] = make_float4(s, s, s, s);
-  } else if (kind == 2) {
-    for (; i + (kProbeUnroll - 1) * stride < n4; i += kProbeUnroll * stride) {
-      float4 v[kProbeUnroll];
+    for (int u = 0; u < kProbeUnroll; ++u) acc += x[u];
+  }
+  for (; i < n4; i += stride) acc += b[i];
+  if (acc.x == 1234.5f) sink[0] = acc;  // keeps the loads alive; practically never stores
+}
+
+template <int KIND>  // 1 write, 2 copy, 3 triad
+__global__ __launch_bounds__(256) void probe_stream_kernel(f32x4v_t* __restrict__ a, const f32x4v_t* __restrict__ b,
+                                                           const f32x4v_t* __restrict__ c, int64_t n4, float s) {
+  const int64_t per = (n4 + gridDim.x - 1) / gridDim.x;
+  const int64_t beg = int64_t(blockIdx.x) * per;
+  const int64_t end = beg + per < n4 ? beg + per : n4;
+  for (int64_t i = beg + threadIdx.x; i < end; i += 256 * kProbeUnroll) {
+    f32x4v_t x[kProbeUnroll], y[kProbeUnroll];
 #pragma unroll
-      for (int u = 0; u < kProbeUnroll; ++u) v[u] = b[i + u * stride];
-#pragma unroll
-      for (int u = 0; u < kProbeUnroll; ++u) a[i + u * stride] = v[u];
-    }
-    for (; i < n4; i += stride) a[i] = b[i];
-  } else {
-    for (; i + (kProbeUnroll - 1) * stride < n4; i += kProbeUnroll * stride) {
-      float4 x[kProbeUnroll], y[kProbeUnroll];
-#pragma unroll
-      for (int u = 0; u < kProbeUnroll; ++u) {
-        x[u] = b[i + u * stride];
-        y[u] = c[i + u * stride];
+    for (int u = 0; u < kProbeUnroll; ++u) {
+      const int64_t j = i + u * 256;
+      if (j < end) {
+        if (KIND >= 2) x[u] = b[j];
+        if (KIND == 3) y[u] = c[j];
       }
-#pragma unroll
-      for (int u = 0; u < kProbeUnroll; ++u)
-        a[i + u * stride] = make_float4(fmaf(s, y[u].x, x[u].x), fmaf(s, y[u].y, x[u].y), fmaf(s, y[u].z, x[u].z),
-                                        fmaf(s, y[u].w, x[u].w));
     }
-    for (; i < n4; i += stride) {
-      const float4 x = b[i], y = c[i];
-      a[i] = make_float4(fmaf(s, y.x, x.x), fmaf(s, y.y, x.y), fmaf(s, y.z, x.z), fmaf(s, y.w, x.w));
+#pragma unroll
+    for (int u = 0; u < kProbeUnroll; ++u) {
+      const int64_t j = i + u * 256;
+      if (j >= end) continue;
+      if (KIND == 1) __builtin_nontemporal_store(f32x4v_t{s, s, s, s}, a + j);
+      else if (KIND == 2) __builtin_nontemporal_store(x[u], a + j);
+      else __builtin_nontemporal_store(x[u] + s * y[u], a + j);
     }
   }
 }
@@ -411,8 +408,15 @@ extern "C" int ezops_hbm_probe(int kind, float* a, const float* b, const float* 
   EZ_REQUIRE(kind >= 0 && kind <= 3, "hbm_probe: kind must be 0..3");
   EZ_REQUIRE(a && (kind == 1 || b) && (kind != 3 || c), "hbm_probe: null pointer");
   EZ_REQUIRE(n >= 4 && n % 4 == 0, "hbm_probe: n must be a positive multiple of 4");
-  const int64_t blocks = int64_t(num_cus()) * 16;
-  hipLaunchKernelGGL(probe_kernel, dim3(unsigned(blocks)), dim3(256), 0, s, kind, reinterpret_cast<float4*>(a),
-                     reinterpret_cast<const float4*>(b), reinterpret_cast<const float4*>(c), n / 4, sc);
+  const dim3 grid{unsigned(num_cus() * 16), 1, 1}, block{256, 1, 1};
+  auto A = reinterpret_cast<f32x4v_t*>(a);
+  auto Bv = reinterpret_cast<const f32x4v_t*>(b);
+  auto Cv = reinterpret_cast<const f32x4v_t*>(c);
+  switch (kind) {
+    case 0: hipLaunchKernelGGL(probe_read_kernel, dim3(unsigned(num_cus() * 4)), block, 0, s, Bv, n / 4, A); break;
+    case 1: hipLaunchKernelGGL(probe_stream_kernel<1>, grid, block, 0, s, A, Bv, Cv, n / 4, sc); break;
+    case 2: hipLaunchKernelGGL(probe_stream_kernel<2>, grid, block, 0, s, A, Bv, Cv, n / 4, sc); break;
+    default: hipLaunchKernelGGL(probe_stream_kernel<3>, grid, block, 0, s, A, Bv, Cv, n / 4, sc); break;
+  }
   return launch_status("hbm_probe");
 }
