@@ -1,41 +1,15 @@
-// Split-KV GQA decode attention for one query token per sequence.
-//
-// Work unit = (sequence b, kv head, split).  One block of W waves owns a
-// contiguous chunk of KV positions of one (b, kv head); its G = H / Hkv query
-// heads share every K/V byte it loads, so K/V cross HBM once per GQA group.
-// Each wave walks 32-position tiles:
-//   * scores S[h, p] = q_h . k_p on MFMA (v_mfma_f32_16x16x32_bf16): A = the
-//     G query rows (zero-padded to 16), B = 16 positions of K per sub-tile;
-//     lanes load 16-byte pieces of K rows straight into the B operand.
-//   * online softmax in the exp2 domain (scale * log2 e folded into S), the
-//     running max kept wave-uniform, row maxima by DPP.
-//   * O += P . V on VALU: V rows are read with fully coalesced 16-byte loads
-//     (one wave instruction covers 1 KiB of consecutive rows); P goes through
-//     a small LDS slice per wave and is read back as broadcasts.
-//   * the next tile's K is requested right after the MFMAs and the next V
-//     right after the P.V update, so loads overlap the softmax / FMA work.
-// The W waves merge their (max, sum, O) through LDS.  With more than one
-// split, the block hands an fp32 partial to the last block of its unit
-// (device-scope arrival counter, sc1 stores/loads, no cache flushes), which
-// merges all splits with every partial load in flight at once.
-//
-// Few units (small batch) use 8-wave blocks and at most 32 splits; many
-// units use 4-wave blocks.
-#include "common.h"
-#include "internal.h"
+// Standalone split-KV GQA decode attention kernel and its launcher.  The
+// per-block routine (and its design notes) is in attn_impl.h.
+#include "attn_impl.h"
 #include "status.h"
 #include "../../include/ezops_hip.h"
-
-#ifndef EZ_ATTN_TILE
-#define EZ_ATTN_TILE 32
-#endif
 
 namespace ez {
 namespace {
 
-constexpr int kTile = EZ_ATTN_TILE;  // positions per wave iteration
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kMaxSplits = 32;       // split partials a merge thread loads at once
+using attn::AttnWs;
+using attn::kMaxSplits;
+using attn::kTile;
 
 int num_cus() {
   static int cus = 0;
@@ -72,343 +46,15 @@ SplitPlan plan_splits(int64_t B, int64_t Hkv, int64_t S, int64_t G) {
   return {waves, ns, chunk};
 }
 
-struct AttnWs {
-  float* opart;   // [B, H, nsplit, D]
-  float* ml;      // [B, H, nsplit, 2]  (max, sum)
-  int* counters;  // [B * Hkv]
-};
-
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
-// K rows enter the MFMA B operand with k-slot (lg, e) of sub-step s mapped to
-// head dim s*32 + lg*8 + e: one wave load instruction then reads, for each of
-// its 16 positions, 64 contiguous bytes (4 lanes x 16 B).  The Q operand uses
-// the same mapping, so the contraction is unchanged.
-template <int D, int NSUB>
-__device__ __forceinline__ void load_k_tile(const uint16_t* Kb, int64_t t0, int64_t last, int li, int lg,
-                                            uint4 (&kf)[NSUB][D / 32]) {
-#pragma unroll
-  for (int u = 0; u < NSUB; ++u) {
-    int64_t p = t0 + 16 * u + li;
-    p = p < last ? p : last;
-    const uint16_t* row = Kb + p * D + lg * 8;
-#pragma unroll
-    for (int s = 0; s < D / 32; ++s) kf[u][s] = ld16_stream(row + 32 * s);
-  }
-}
-
-// V rows in row layout: lane (dc, rs) reads rows rs, rs + RPI, ... of the tile,
-// 16 B at column 8*dc; one wave instruction covers RPI consecutive rows.
-template <int D, int NPV>
-__device__ __forceinline__ void load_v_tile(const uint16_t* Vb, int64_t t0, int64_t last, int dc, int rs,
-                                            uint4 (&vf)[NPV]) {
-  constexpr int RPI = kWave / (D / 8);
-#pragma unroll
-  for (int j = 0; j < NPV; ++j) {
-    int64_t p = t0 + rs + RPI * j;
-    p = p < last ? p : last;
-    vf[j] = ld16_stream(Vb + p * D + dc * 8);
-  }
-}
-
-// Qwen3 per-head RMSNorm (fp32 statistics, weight) + half-split RoPE of one
-// head held in bf16 at `src`, rounded once to bf16 into `dst` (LDS or global).
-// One wave; lane l owns the pairs (i, i + D/2), i = l, l + 64, ...  Operation
-// order follows the reference (ezops/ops/fused_qk_norm_rope.py:138-147).
-template <int D>
-__device__ __forceinline__ void norm_rope_head(const uint16_t* src, const uint16_t* w, const uint16_t* crow,
-                                               const uint16_t* srow, float eps, uint16_t* dst, int lane) {
-  constexpr int HALF = D / 2;
-  constexpr int NP = (HALF + kWave - 1) / kWave;
-  float x1[NP], x2[NP];
-  float ss = 0.f;
-#pragma unroll
-  for (int t = 0; t < NP; ++t) {
-    const int i = lane + t * kWave;
-    x1[t] = i < HALF ? bf2f(src[i]) : 0.f;
-    x2[t] = i < HALF ? bf2f(src[i + HALF]) : 0.f;
-    ss += x1[t] * x1[t] + x2[t] * x2[t];
-  }
-  const float r = rsqrtf(wave_sum(ss) / float(D) + eps);
-#pragma unroll
-  for (int t = 0; t < NP; ++t) {
-    const int i = lane + t * kWave;
-    if (i >= HALF) break;
-    float y1 = __fmul_rn(x1[t], r), y2 = __fmul_rn(x2[t], r);
-    if (w) {
-      y1 = __fmul_rn(y1, bf2f(w[i]));
-      y2 = __fmul_rn(y2, bf2f(w[i + HALF]));
-    }
-    float o1 = y1, o2 = y2;
-    if (crow) {
-      o1 = __fadd_rn(__fmul_rn(y1, bf2f(crow[i])), __fmul_rn(-y2, bf2f(srow[i])));
-      o2 = __fadd_rn(__fmul_rn(y2, bf2f(crow[i + HALF])), __fmul_rn(y1, bf2f(srow[i + HALF])));
-    }
-    dst[i] = f2bf(o1);
-    dst[i + HALF] = f2bf(o2);
-  }
-}
-
-template <int D, int G, int W, bool LAYER>
+template <int D, int G, int W, int QSRC>
 __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int64_t nsplit, int64_t chunk,
                                                                AttnWs ws) {
-  constexpr int NT = W * kWave;      // threads per block
-  constexpr int NS = D / 32;         // MFMA k-steps per 16-position sub-tile
-  constexpr int CPR = D / 8;         // 16-byte chunks per K/V row
-  constexpr int RPI = kWave / CPR;   // rows covered by one wave-wide V load
-  constexpr int NSUB = kTile / 16;   // MFMA sub-tiles per tile
-  constexpr int NPV = kTile / RPI;   // V rows per lane per tile
-  constexpr int GP = G <= 4 ? 4 : 8; // P row stride in LDS (float4 reads)
-  static_assert(G <= 8, "group size");
-
-  __shared__ __align__(16) float Ps[W][kTile][GP];
-  __shared__ __align__(16) float Os[W][G][D];
-  __shared__ float Ms[W][G], Ls[W][G];
-  __shared__ float Wt[G][kMaxSplits];
-  __shared__ __align__(16) uint16_t Qs[LAYER ? G : 1][D];
-
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
-  const int li = lane & 15, lg = lane >> 4;
-  const int64_t split = blockIdx.x % nsplit;
-  const int64_t unit = blockIdx.x / nsplit;
-  const int64_t kvh = unit % a.Hkv, b = unit / a.Hkv;
-  int64_t L = a.kv_lens ? int64_t(a.kv_lens[b]) : a.S;
-  L = L < 0 ? 0 : (L > a.S ? a.S : L);
-  const int64_t p_begin = split * chunk;
-  const int64_t p_end = (p_begin + chunk < L) ? p_begin + chunk : L;
-  const int64_t last = p_end - 1;
-
-  const uint16_t* Kb = a.K + (b * a.Hkv + kvh) * a.S * D;
-  const uint16_t* Vb = a.V + (b * a.Hkv + kvh) * a.S * D;
-  const int64_t h0 = kvh * G;  // first query head of the group
-  const float sl2 = a.scale * kLog2e;
-  const int dc = lane % CPR, rs = lane / CPR;
-
-  // The block whose chunk holds the decoded token writes its k/v first and
-  // only then loads K/V tiles; every other block starts its loads at once.
-  const int64_t pos = L - 1;
-  const bool owner = LAYER && pos >= p_begin && pos < p_end;
-  int64_t t0 = p_begin + int64_t(wave) * kTile;
-  uint4 kf[NSUB][NS], vf[NPV];
-  if (!owner && t0 < p_end) {
-    load_k_tile<D, NSUB>(Kb, t0, last, li, lg, kf);
-    load_v_tile<D, NPV>(Vb, t0, last, dc, rs, vf);
-  }
-
-  bf16x8_t qf[NS];
-  if constexpr (LAYER) {
-    if (L > 0) {
-      const uint16_t* row = a.qkv + b * a.qkv_bs;
-      const uint16_t* crow = a.cos ? a.cos + pos * D : nullptr;
-      const uint16_t* srow = a.sin ? a.sin + pos * D : nullptr;
-      for (int h = wave; h < G; h += W)
-        norm_rope_head<D>(row + (h0 + h) * D, a.qw, crow, srow, a.eps, &Qs[h][0], lane);
-      if (owner && wave == W - 1) {
-        const int64_t kofs = a.H * D + kvh * D, vofs = (a.H + a.Hkv) * D + kvh * D;
-        uint16_t* kdst = const_cast<uint16_t*>(Kb) + pos * D;
-        uint16_t* vdst = const_cast<uint16_t*>(Vb) + pos * D;
-        norm_rope_head<D>(row + kofs, a.kw, crow, srow, a.eps, kdst, lane);
-        for (int i = lane; i < D; i += kWave) vdst[i] = row[vofs + i];
-      }
-    }
-    __syncthreads();  // Qs complete; the cache slot written by this block is visible to it
-    if (owner && t0 < p_end) {
-      load_k_tile<D, NSUB>(Kb, t0, last, li, lg, kf);
-      load_v_tile<D, NPV>(Vb, t0, last, dc, rs, vf);
-    }
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (li < G) v = *reinterpret_cast<const uint4*>(&Qs[li][32 * s + lg * 8]);
-      qf[s] = as_bf16x8(v);
-    }
-  } else {
-    // Q operand: lane (li, lg) holds Q[h0 + li][s*32 + lg*8 .. +8] for step s.
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (li < G) v = *reinterpret_cast<const uint4*>(a.Q + ((b * a.H + h0 + li) * D) + 32 * s + lg * 8);
-      qf[s] = as_bf16x8(v);
-    }
-  }
-
-  float m_run[G], l_acc[G], o[G][8];
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    m_run[h] = -INFINITY;
-    l_acc[h] = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
-  }
-
-  for (; t0 < p_end; t0 += int64_t(W) * kTile) {
-    const int64_t tn = t0 + int64_t(W) * kTile;
-    // ---- scores: acc[u][j] = S[head 4*lg + j][pos t0 + 16u + li]
-    f32x4_t acc[NSUB];
-#pragma unroll
-    for (int u = 0; u < NSUB; ++u) {
-      acc[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < NS; ++s)
-        acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf[s], as_bf16x8(kf[u][s]), acc[u], 0, 0, 0);
-    }
-    if (tn < p_end) load_k_tile<D, NSUB>(Kb, tn, last, li, lg, kf);  // next K while this tile finishes
-
-    float mx[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      mx[j] = -INFINITY;
-#pragma unroll
-      for (int u = 0; u < NSUB; ++u) {
-        const bool ok = t0 + 16 * u + li < p_end;
-        const float sv = ok ? acc[u][j] * sl2 : -INFINITY;
-        acc[u][j] = sv;
-        mx[j] = fmaxf(mx[j], sv);
-      }
-      mx[j] = dpp_row16<true>(mx[j]);
-    }
-    // ---- wave-uniform running max and rescale factors
-    float m_use[G];
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float mt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx[h & 3]), 16 * (h >> 2)));
-      const float mn = fmaxf(m_run[h], mt);
-      const float alpha = (m_run[h] == -INFINITY) ? 0.f : exp2f(m_run[h] - mn);
-      m_run[h] = mn;
-      m_use[h] = (mn == -INFINITY) ? 0.f : mn;
-      l_acc[h] *= alpha;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[h][e] *= alpha;
-    }
-    // ---- P = exp2(S - m) into LDS as Ps[pos][head]
-    if (lg < GP / 4) {
-#pragma unroll
-      for (int u = 0; u < NSUB; ++u) {
-        float pv[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int h = 4 * lg + j;
-          float mu = m_use[j < G ? j : 0];
-          if constexpr (G > 4) mu = (lg == 1) ? m_use[4 + j] : mu;
-          pv[j] = (h < G) ? exp2f(acc[u][j] - mu) : 0.f;
-        }
-        *reinterpret_cast<float4*>(&Ps[wave][16 * u + li][4 * lg]) = make_float4(pv[0], pv[1], pv[2], pv[3]);
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // ---- O += P . V
-#pragma unroll
-    for (int j = 0; j < NPV; ++j) {
-      float pr[GP];
-#pragma unroll
-      for (int q4 = 0; q4 < GP / 4; ++q4) {
-        const float4 t = *reinterpret_cast<const float4*>(&Ps[wave][rs + RPI * j][4 * q4]);
-        pr[4 * q4 + 0] = t.x; pr[4 * q4 + 1] = t.y; pr[4 * q4 + 2] = t.z; pr[4 * q4 + 3] = t.w;
-      }
-      float v[8];
-      unpack8(vf[j], v);
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        l_acc[h] += pr[h];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[h][e] = fmaf(pr[h], v[e], o[h][e]);
-      }
-    }
-    if (tn < p_end) load_v_tile<D, NPV>(Vb, tn, last, dc, rs, vf);  // next V
-    __builtin_amdgcn_wave_barrier();
-  }
-
-  // ---- merge the row groups of the wave (lanes with equal dc)
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-#pragma unroll
-    for (int off = CPR; off < kWave; off <<= 1) {
-      l_acc[h] += __shfl_xor(l_acc[h], off, kWave);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[h][e] += __shfl_xor(o[h][e], off, kWave);
-    }
-  }
-  if (rs == 0) {
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      *reinterpret_cast<float4*>(&Os[wave][h][dc * 8]) = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
-      *reinterpret_cast<float4*>(&Os[wave][h][dc * 8 + 4]) = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
-    }
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      Ms[wave][h] = m_run[h];
-      Ls[wave][h] = l_acc[h];
-    }
-  }
-  __syncthreads();
-
-  // ---- merge the W waves: thread handles (h, d) pairs
-  for (int idx = threadIdx.x; idx < G * D; idx += NT) {
-    const int h = idx / D, d = idx % D;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < W; ++w) M = fmaxf(M, Ms[w][h]);
-    float ov = 0.f, lv = 0.f;
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-      const float f = (Ms[w][h] == -INFINITY) ? 0.f : exp2f(Ms[w][h] - M);
-      ov = fmaf(f, Os[w][h][d], ov);
-      lv = fmaf(f, Ls[w][h], lv);
-    }
-    const int64_t hq = b * a.H + h0 + h;
-    if (nsplit == 1) {
-      a.Out[hq * D + d] = f2bf(lv > 0.f ? ov / lv : 0.f);
-    } else {
-      st_dev(ws.opart + (hq * nsplit + split) * D + d, ov);
-      if (d == 0) {
-        st_dev(ws.ml + (hq * nsplit + split) * 2 + 0, M);
-        st_dev(ws.ml + (hq * nsplit + split) * 2 + 1, lv);
-      }
-    }
-  }
-  if (nsplit == 1) return;
-  if (!arrive_last(ws.counters + unit, int(nsplit))) return;
-
-  // ---- last block of the unit merges the splits.
-  // (1) per head: one wave reads the nsplit (max, sum) pairs at once and
-  //     turns them into normalised weights w_s = 2^(m_s - M) / sum.
-  for (int h = wave; h < G; h += W) {
-    const int64_t hq = b * a.H + h0 + h;
-    const float* ml = ws.ml + hq * nsplit * 2;
-    const bool ok = lane < nsplit;
-    const float ms = ok ? ld_dev(ml + 2 * lane) : -INFINITY;
-    const float ls = ok ? ld_dev(ml + 2 * lane + 1) : 0.f;
-    const float M = wave_reduce_uniform<true>(ms);
-    const float f = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
-    const float tot = wave_reduce_uniform<false>(f * ls);
-    if (ok) Wt[h][lane] = tot > 0.f ? f / tot : 0.f;
-  }
-  __syncthreads();
-  // (2) thread per (h, d): weighted sum of the split partials; all nsplit
-  //     loads of a thread are issued before the first is used.
-  for (int idx = threadIdx.x; idx < G * D; idx += NT) {
-    const int h = idx / D, d = idx % D;
-    const int64_t hq = b * a.H + h0 + h;
-    const float* op = ws.opart + hq * nsplit * D + d;
-    constexpr int CB = G > 4 ? kMaxSplits / 2 : kMaxSplits;  // loads in flight (register budget)
-    float acc = 0.f;
-    for (int s0 = 0; s0 < nsplit; s0 += CB) {
-      float v[CB];
-#pragma unroll
-      for (int e = 0; e < CB; ++e) v[e] = s0 + e < nsplit ? ld_dev(op + (s0 + e) * D) : 0.f;
-#pragma unroll
-      for (int e = 0; e < CB; ++e)
-        if (s0 + e < nsplit) acc = fmaf(Wt[h][s0 + e], v[e], acc);
-    }
-    a.Out[hq * D + d] = f2bf(acc);
-  }
+  attn::attn_block<D, G, W, QSRC, attn::kOutBf16>(a, blockIdx.x % nsplit, blockIdx.x / nsplit, nsplit, chunk, ws);
 }
 
-template <int D, int W, bool LAYER>
+template <int D, int W, int LAYER>
 void launch_dw(const AttnArgs& a, const SplitPlan& pl, const AttnWs& ws, int64_t G, hipStream_t s) {
   const dim3 grid{unsigned(a.B * a.Hkv * pl.nsplit), 1, 1}, block{unsigned(W * kWave), 1, 1};
   switch (G) {
@@ -419,7 +65,7 @@ void launch_dw(const AttnArgs& a, const SplitPlan& pl, const AttnWs& ws, int64_t
   }
 }
 
-template <int D, bool LAYER>
+template <int D, int LAYER>
 void launch_d(const AttnArgs& a, const SplitPlan& pl, const AttnWs& ws, int64_t G, hipStream_t s) {
   const dim3 block{unsigned(pl.waves * kWave), 1, 1};
   const dim3 grid{unsigned(a.B * a.Hkv * pl.nsplit), 1, 1};
@@ -466,11 +112,11 @@ int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
   AttnArgs aa = a;
   if (aa.scale <= 0.f) aa.scale = 1.0f / sqrtf(float(a.D));
   if (layer) {
-    if (a.D == 64) launch_d<64, true>(aa, pl, w, G, s);
-    else launch_d<128, true>(aa, pl, w, G, s);
+    if (a.D == 64) launch_d<64, attn::kQFromQkvBf16>(aa, pl, w, G, s);
+    else launch_d<128, attn::kQFromQkvBf16>(aa, pl, w, G, s);
   } else {
-    if (a.D == 64) launch_d<64, false>(aa, pl, w, G, s);
-    else launch_d<128, false>(aa, pl, w, G, s);
+    if (a.D == 64) launch_d<64, attn::kQFromQ>(aa, pl, w, G, s);
+    else launch_d<128, attn::kQFromQ>(aa, pl, w, G, s);
   }
   return launch_status("attn_decode");
 }

@@ -11,6 +11,9 @@
 //                  out = o_proj + FFN(attn, hidden)
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
+#include <cstring>
+
 #include "internal.h"
 #include "status.h"
 #include "../../include/ezops_hip.h"
@@ -83,12 +86,29 @@ extern "C" int ezops_o_proj_ffn_bf16(const void* attn, const void* residual, con
                  static_cast<char*>(ws), s);
 }
 
-extern "C" size_t ezops_qwen3_layer_workspace_size(const ezops_qwen3_layer* p) {
-  if (!p) return 0;
+namespace {
+// EZOPS_LAYER_PERSISTENT=1 selects the persistent single-launch layer
+// (layer.hip) where supported.  It is off by default: on MI355X its grid
+// barriers cost 8-13 us each (cross-XCD hand-offs through memory), more than
+// the ~1 us kernel boundaries of the multi-kernel graph it replaces.
+bool persistent_enabled() {
+  const char* e = std::getenv("EZOPS_LAYER_PERSISTENT");
+  return e && std::strcmp(e, "1") == 0;
+}
+
+size_t multi_kernel_ws(const ezops_qwen3_layer* p) {
   const int64_t QR = p->H * p->D, KVR = p->Hkv * p->D;
   return align256(size_t(p->B * (QR + 2 * KVR)) * 2)   // qkv
          + align256(size_t(p->B * QR) * 2)              // attention output
          + align256(attn_workspace_size(p->B, p->H, p->Hkv, p->S, p->D)) + ffn_ws(p->B, p->HS, p->IS);
+}
+}  // namespace
+
+extern "C" size_t ezops_qwen3_layer_workspace_size(const ezops_qwen3_layer* p) {
+  if (!p || p->B < 1 || p->H < 1 || p->Hkv < 1 || p->D < 1) return 0;
+  // Disjoint regions for the two paths (the persistent one is chosen per
+  // call), so neither path ever sees the other's data in its counters.
+  return align256(multi_kernel_ws(p)) + layer_persistent_ws(*p);
 }
 
 extern "C" int ezops_qwen3_dense_decode_bf16(const ezops_qwen3_layer* p, void* ws, size_t ws_bytes,
@@ -101,6 +121,8 @@ extern "C" int ezops_qwen3_dense_decode_bf16(const ezops_qwen3_layer* p, void* w
   EZ_REQUIRE(p->H % p->Hkv == 0, "qwen3_dense_decode: num_heads must be divisible by num_kv_heads");
   EZ_REQUIRE((p->cos == nullptr) == (p->sin == nullptr), "qwen3_dense_decode: cos and sin go together");
   EZ_REQUIRE(ws_bytes >= ezops_qwen3_layer_workspace_size(p), "qwen3_dense_decode: workspace too small");
+  if (persistent_enabled() && layer_persistent_supported(*p))
+    return launch_layer_persistent(*p, static_cast<char*>(ws) + align256(multi_kernel_ws(p)), s);
   const int64_t QR = p->H * p->D, KVR = p->Hkv * p->D, QKV = QR + 2 * KVR;
   Carve c{static_cast<char*>(ws)};
   uint16_t* qkv = c.take<uint16_t>(size_t(p->B * QKV) * 2);
