@@ -230,6 +230,8 @@ def profile_only(torch, _hip, flush, args) -> int:
         op, data, lens = layer_workload(torch, args.batch)
         HS, IS = 4096, 12288
         h = torch.empty(args.batch, IS, dtype=torch.bfloat16, device="cuda")
+        ws = torch.zeros(max(256, _hip.size("ezops_linear_stage_workspace_size", args.batch, HS, 1)),
+                         dtype=torch.uint8, device="cuda")
         for _ in range(10):
             flush()
             if args.profile_kernel == "layer":
@@ -238,7 +240,7 @@ def profile_only(torch, _hip, flush, args) -> int:
                 Wgu = data[5]
                 _hip.call("ezops_linear_stage_bf16", data[0].data_ptr(), HS, Wgu.data_ptr(), Wgu[IS:].data_ptr(),
                           h.data_ptr(), IS, None, 0, data[10].data_ptr(), 1, 1e-6, 2, args.batch, IS, HS,
-                          _hip.stream())
+                          ws.data_ptr(), ws.numel(), _hip.stream())
     torch.cuda.synchronize()
     log(f"profile run of {args.profile_kernel} done")
     return 0
@@ -304,13 +306,16 @@ def main() -> int:
     x2, post_w = data[0], data[10]
     copies = [data[5]] + [data[5].clone() for _ in range(2)]
     h = torch.empty(B, IS, dtype=torch.bfloat16, device="cuda")
+    ws = torch.zeros(max(256, _hip.size("ezops_linear_stage_workspace_size", B, HS, 1)), dtype=torch.uint8,
+                     device="cuda")
     n_launch = 12
 
     def gate_up_chain():  # launched on the current (capturing) stream
         for i in range(n_launch):
             W = copies[i % len(copies)]
             _hip.call("ezops_linear_stage_bf16", x2.data_ptr(), HS, W.data_ptr(), W[IS:].data_ptr(), h.data_ptr(),
-                      IS, None, 0, post_w.data_ptr(), 1, 1e-6, 2, B, IS, HS, _hip.stream())
+                      IS, None, 0, post_w.data_ptr(), 1, 1e-6, 2, B, IS, HS, ws.data_ptr(), ws.numel(),
+                      _hip.stream())
 
     gu_ms = statistics.mean(time_graph(gate_up_chain, max(5, args.steps // 3), 2, flush_cache)) / n_launch
     gu_bytes = 2 * IS * HS * 2 + B * HS * 2 + HS * 2 + B * IS * 2

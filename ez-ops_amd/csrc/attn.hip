@@ -51,7 +51,14 @@ size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 template <int D, int G, int W, int QSRC>
 __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int64_t nsplit, int64_t chunk,
                                                                AttnWs ws) {
-  attn::attn_block<D, G, W, QSRC, attn::kOutBf16>(a, blockIdx.x % nsplit, blockIdx.x / nsplit, nsplit, chunk, ws);
+  attn::attn_block<D, G, W, QSRC, attn::kOutBf16, false>(a, blockIdx.x % nsplit, blockIdx.x / nsplit, nsplit, chunk,
+                                                        ws);
+}
+
+// One wave per query head merges that head's split partials.
+template <int D>
+__global__ __launch_bounds__(kWave) void attn_combine_kernel(AttnArgs a, int64_t nsplit, AttnWs ws) {
+  attn::attn_combine<D, attn::kOutBf16>(a, blockIdx.x, nsplit, ws);
 }
 
 template <int D, int W, int LAYER>
@@ -117,6 +124,11 @@ int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
   } else {
     if (a.D == 64) launch_d<64, attn::kQFromQ>(aa, pl, w, G, s);
     else launch_d<128, attn::kQFromQ>(aa, pl, w, G, s);
+  }
+  if (pl.nsplit > 1) {
+    const dim3 grid{unsigned(a.B * a.H), 1, 1}, block{kWave, 1, 1};
+    if (a.D == 64) hipLaunchKernelGGL(attn_combine_kernel<64>, grid, block, 0, s, aa, pl.nsplit, w);
+    else hipLaunchKernelGGL(attn_combine_kernel<128>, grid, block, 0, s, aa, pl.nsplit, w);
   }
   return launch_status("attn_decode");
 }

@@ -125,7 +125,12 @@ __device__ __forceinline__ void norm_rope_head(const T* src, const uint16_t* w, 
   }
 }
 
-template <int D, int G, int W, int QSRC, int OUT>
+// MERGE_LAST: with more than one split, the last block of a unit merges all
+// splits in this launch (device-coherent hand-off + arrival counter).
+// Otherwise blocks store plain fp32 partials and attn_combine() merges them
+// in a following launch (the kernel boundary orders the hand-off, which is
+// cheaper than the in-kernel store -> wait -> count -> load chain).
+template <int D, int G, int W, int QSRC, int OUT, bool MERGE_LAST>
 __device__ __forceinline__ void attn_block(const AttnArgs& a, int64_t split, int64_t unit, int64_t nsplit,
                                            int64_t chunk, const AttnWs& ws) {
   constexpr bool LAYER = QSRC != kQFromQ;
@@ -147,28 +152,33 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, int64_t split, int
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
   const int64_t kvh = unit % a.Hkv, b = unit / a.Hkv;
-  int64_t L = a.kv_lens ? int64_t(a.kv_lens[b]) : a.S;
-  L = L < 0 ? 0 : (L > a.S ? a.S : L);
-  const int64_t p_begin = split * chunk;
-  const int64_t p_end = (p_begin + chunk < L) ? p_begin + chunk : L;
-  const int64_t last = p_end - 1;
-
   const uint16_t* Kb = a.K + (b * a.Hkv + kvh) * a.S * D;
   const uint16_t* Vb = a.V + (b * a.Hkv + kvh) * a.S * D;
   const int64_t h0 = kvh * G;  // first query head of the group
   const float sl2 = a.scale * kLog2e;
   const int dc = lane % CPR, rs = lane / CPR;
+  const int64_t p_begin = split * chunk;
 
-  // The block whose chunk holds the decoded token writes its k/v first and
-  // only then loads K/V tiles; every other block starts its loads at once.
+  // The first tile is requested before the sequence length arrives: its
+  // addresses only need the cache capacity (clamped to slot S-1), and rows at
+  // or beyond the real length are masked below (scores to -inf, V rows to 0).
+  int64_t t0 = p_begin + int64_t(wave) * kTile;
+  const int64_t spec_end = (p_begin + chunk < a.S) ? p_begin + chunk : a.S;
+  uint4 kf[NSUB][NS], vf[NPV];
+  if (t0 < spec_end) {
+    load_k_tile<D, NSUB>(Kb, t0, spec_end - 1, li, lg, kf);
+    load_v_tile<D, NPV>(Vb, t0, spec_end - 1, dc, rs, vf);
+  }
+
+  int64_t L = a.kv_lens ? int64_t(a.kv_lens[b]) : a.S;
+  L = L < 0 ? 0 : (L > a.S ? a.S : L);
+  const int64_t p_end = (p_begin + chunk < L) ? p_begin + chunk : L;
+  const int64_t last = p_end - 1;
+
+  // The block whose chunk holds the decoded token writes its k/v slot and
+  // then reloads its first tile, which may have been read before the write.
   const int64_t pos = L - 1;
   const bool owner = LAYER && pos >= p_begin && pos < p_end;
-  int64_t t0 = p_begin + int64_t(wave) * kTile;
-  uint4 kf[NSUB][NS], vf[NPV];
-  if (!owner && t0 < p_end) {
-    load_k_tile<D, NSUB>(Kb, t0, last, li, lg, kf);
-    load_v_tile<D, NPV>(Vb, t0, last, dc, rs, vf);
-  }
 
   bf16x8_t qf[NS];
   if constexpr (LAYER) {
@@ -194,8 +204,8 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, int64_t split, int
     }
     __syncthreads();  // Qs complete; the cache slot written by this block is visible to it
     if (owner && t0 < p_end) {
-      load_k_tile<D, NSUB>(Kb, t0, last, li, lg, kf);
-      load_v_tile<D, NPV>(Vb, t0, last, dc, rs, vf);
+      load_k_tile<D, NSUB>(Kb, t0, spec_end - 1, li, lg, kf);
+      load_v_tile<D, NPV>(Vb, t0, spec_end - 1, dc, rs, vf);
     }
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
@@ -290,6 +300,10 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, int64_t split, int
       }
       float v[8];
       unpack8(vf[j], v);
+      if (t0 + rs + RPI * j >= p_end) {  // masked row: its cache bytes may be anything
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.f;
+      }
 #pragma unroll
       for (int h = 0; h < G; ++h) {
         l_acc[h] += pr[h];
@@ -345,14 +359,18 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, int64_t split, int
       const float r = lv > 0.f ? ov / lv : 0.f;
       if constexpr (OUT == kOutF32Dev) st_dev(a.out_f + hq * D + d, round_bf(r));
       else a.Out[hq * D + d] = f2bf(r);
-    } else {
+    } else if constexpr (MERGE_LAST) {
       st_dev(ws.opart + (hq * nsplit + split) * D + d, ov);
       if (d == 0) {
         st_dev(ws.ml + (hq * nsplit + split) * 2 + 0, M);
         st_dev(ws.ml + (hq * nsplit + split) * 2 + 1, lv);
       }
+    } else {
+      ws.opart[(hq * nsplit + split) * D + d] = ov;
+      if (d == 0) *reinterpret_cast<float2*>(ws.ml + (hq * nsplit + split) * 2) = make_float2(M, lv);
     }
   }
+  if constexpr (!MERGE_LAST) return;
   if (nsplit == 1) return;
   if (!arrive_last(ws.counters + unit, int(nsplit))) return;
 
@@ -389,6 +407,42 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, int64_t split, int
     }
     if constexpr (OUT == kOutF32Dev) st_dev(a.out_f + hq * D + d, round_bf(acc));
     else a.Out[hq * D + d] = f2bf(acc);
+  }
+}
+
+// Merge of the split partials of one query head (b, h): one wave, lane s
+// reads split s's (max, sum); every lane reads its head dims of all splits at
+// once.  out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
+template <int D, int OUT>
+__device__ __forceinline__ void attn_combine(const AttnArgs& a, int64_t hq, int64_t nsplit, const AttnWs& ws) {
+  constexpr int DPL = D / kWave;  // head dims per lane
+  const int lane = threadIdx.x & (kWave - 1);
+  const float* op = ws.opart + hq * nsplit * D;
+  const float* ml = ws.ml + hq * nsplit * 2;
+  const bool ok = lane < nsplit;
+  const float2 st = ok ? *reinterpret_cast<const float2*>(ml + 2 * lane) : make_float2(-INFINITY, 0.f);
+  float acc[DPL];
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) {
+    float v[kMaxSplits];
+#pragma unroll
+    for (int s = 0; s < kMaxSplits; ++s) v[s] = s < nsplit ? op[s * D + lane + e * kWave] : 0.f;
+    const float M = wave_reduce_uniform<true>(st.x);
+    const float f = (st.x == -INFINITY) ? 0.f : exp2f(st.x - M);
+    const float tot = wave_reduce_uniform<false>(f * st.y);
+    const float wgt = tot > 0.f ? f / tot : 0.f;
+    acc[e] = 0.f;
+#pragma unroll
+    for (int s = 0; s < kMaxSplits; ++s) {
+      const float ws_ = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), s));
+      acc[e] = fmaf(ws_, v[s], acc[e]);  // v[s] = 0 and ws_ = 0 for s >= nsplit
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) {
+    const int d = lane + e * kWave;
+    if constexpr (OUT == kOutF32Dev) st_dev(a.out_f + hq * D + d, round_bf(acc[e]));
+    else a.Out[hq * D + d] = f2bf(acc[e]);
   }
 }
 

@@ -34,7 +34,7 @@ struct Carve {
 };
 
 size_t ffn_ws(int64_t B, int64_t HS, int64_t IS) {
-  return align256(size_t(B * HS) * 2) + align256(size_t(B * IS) * 2);
+  return align256(size_t(B * HS) * 2) * 2 + align256(size_t(B * IS) * 2);
 }
 
 int run_ffn(const uint16_t* attn, const uint16_t* residual, const uint16_t* Wo, const uint16_t* post_w,
@@ -43,6 +43,7 @@ int run_ffn(const uint16_t* attn, const uint16_t* residual, const uint16_t* Wo, 
   Carve c{ws};
   uint16_t* x2 = c.take<uint16_t>(size_t(B * HS) * 2);
   uint16_t* h = c.take<uint16_t>(size_t(B * IS) * 2);
+  uint16_t* xn = c.take<uint16_t>(size_t(B * HS) * 2);  // staged RMSNorm input (batch > 4)
 
   LinearArgs o{};
   o.X = attn; o.ldx = QR; o.W = Wo; o.Y = x2; o.ldy = HS;
@@ -53,6 +54,7 @@ int run_ffn(const uint16_t* attn, const uint16_t* residual, const uint16_t* Wo, 
   LinearArgs gu{};
   gu.X = x2; gu.ldx = HS; gu.W = Wg; gu.W2 = Wu; gu.Y = h; gu.ldy = IS;
   gu.M = B; gu.N = IS; gu.K = HS; gu.norm = 1; gu.norm_w = post_w; gu.eps = eps; gu.epi = kEpiSilu;
+  gu.xn_ws = xn;
   rc = launch_linear(gu, s);
   if (rc) return rc;
 
@@ -98,7 +100,8 @@ bool persistent_enabled() {
 
 size_t multi_kernel_ws(const ezops_qwen3_layer* p) {
   const int64_t QR = p->H * p->D, KVR = p->Hkv * p->D;
-  return align256(size_t(p->B * (QR + 2 * KVR)) * 2)   // qkv
+  return align256(size_t(p->B * p->HS) * 2)            // staged RMSNorm input (batch > 4)
+         + align256(size_t(p->B * (QR + 2 * KVR)) * 2)   // qkv
          + align256(size_t(p->B * QR) * 2)              // attention output
          + align256(attn_workspace_size(p->B, p->H, p->Hkv, p->S, p->D)) + ffn_ws(p->B, p->HS, p->IS);
 }
@@ -125,6 +128,7 @@ extern "C" int ezops_qwen3_dense_decode_bf16(const ezops_qwen3_layer* p, void* w
     return launch_layer_persistent(*p, static_cast<char*>(ws) + align256(multi_kernel_ws(p)), s);
   const int64_t QR = p->H * p->D, KVR = p->Hkv * p->D, QKV = QR + 2 * KVR;
   Carve c{static_cast<char*>(ws)};
+  uint16_t* xn = c.take<uint16_t>(size_t(p->B * p->HS) * 2);
   uint16_t* qkv = c.take<uint16_t>(size_t(p->B * QKV) * 2);
   uint16_t* att = c.take<uint16_t>(size_t(p->B * QR) * 2);
   char* attn_ws = c.take<char>(attn_workspace_size(p->B, p->H, p->Hkv, p->S, p->D));
@@ -134,7 +138,7 @@ extern "C" int ezops_qwen3_dense_decode_bf16(const ezops_qwen3_layer* p, void* w
   LinearArgs l{};
   l.X = hidden; l.ldx = p->HS; l.W = static_cast<const uint16_t*>(p->Wqkv); l.Y = qkv; l.ldy = QKV;
   l.M = p->B; l.N = QKV; l.K = p->HS; l.norm = 1; l.norm_w = static_cast<const uint16_t*>(p->in_norm_w);
-  l.eps = p->eps; l.epi = kEpiStore;
+  l.eps = p->eps; l.epi = kEpiStore; l.xn_ws = xn;
   int rc = launch_linear(l, s);
   if (rc) return rc;
 

@@ -26,6 +26,9 @@
 #ifndef EZ_GEMV_U
 #define EZ_GEMV_U 8         // 16-byte chunks per lane in flight per row (M <= 2)
 #endif
+#ifndef EZ_MFMA_INTERLEAVE
+#define EZ_MFMA_INTERLEAVE 0  // 1: wave w takes 128-wide K chunks w, w+4, ... (else a contiguous quarter)
+#endif
 
 namespace ez {
 namespace {
@@ -156,10 +159,40 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_valu_kernel(LinearArgs a) {
 // of a 128-wide chunk) is the same for A and B, so the contraction is
 // exact, and each wave load instruction reads 64 contiguous bytes (4 lanes)
 // of each of its 16 weight rows.
-template <int T, bool NORM, bool SILU>
+template <int T>
+struct MfmaFrag {
+  uint4 w[T][4];
+  uint4 x[4];
+};
+
+template <int T, bool SILU>
+__device__ __forceinline__ void mfma_load(MfmaFrag<T>& f, const uint16_t* const (&wrow)[T], const uint16_t* xrow,
+                                          bool mvalid, int64_t c, int g, int64_t K) {
+  const int64_t kb = c * 128 + g * 8;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int64_t k = kb + s * 32;
+    const bool ok = k < K;
+#pragma unroll
+    for (int t = 0; t < T; ++t) f.w[t][s] = ok ? ld16_stream(wrow[t] + k) : make_uint4(0, 0, 0, 0);
+    f.x[s] = (ok && mvalid) ? *reinterpret_cast<const uint4*>(xrow + k) : make_uint4(0, 0, 0, 0);
+  }
+}
+
+template <int T>
+__device__ __forceinline__ void mfma_step(f32x4_t (&acc)[T], const MfmaFrag<T>& f) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const bf16x8_t bx = as_bf16x8(f.x[s]);
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(f.w[t][s]), bx, acc[t], 0, 0, 0);
+  }
+}
+
+template <int T, bool SILU>
 __global__ __launch_bounds__(kBlock) void linear_mfma_kernel(LinearArgs a) {
   __shared__ float red[kWavesPerBlock][T][4][kWave];
-  __shared__ float ssq[kWavesPerBlock][16];
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const int i = lane & 15, g = lane >> 4;
   const int64_t m0 = int64_t(blockIdx.y) * 16;
@@ -178,52 +211,29 @@ __global__ __launch_bounds__(kBlock) void linear_mfma_kernel(LinearArgs a) {
   const uint16_t* xrow = a.X + (mvalid ? m : 0) * a.ldx;
 
   const int64_t nchunks = (a.K + 127) / 128;
+#if EZ_MFMA_INTERLEAVE
+  const int64_t cb = 0, ce = (nchunks - wave + kWavesPerBlock - 1) / kWavesPerBlock;  // local chunk count
+  auto chunk = [&](int64_t c) { return c * kWavesPerBlock + wave; };
+#else
   const int64_t cb = nchunks * wave / kWavesPerBlock, ce = nchunks * (wave + 1) / kWavesPerBlock;
+  auto chunk = [&](int64_t c) { return c; };
+#endif
 
   f32x4_t acc[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float ss = 0.f;
 
-  for (int64_t c = cb; c < ce; ++c) {
-    const int64_t kb = c * 128 + g * 8;
-    uint4 wv[T][4], xv[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int64_t k = kb + s * 32;
-      const bool ok = k < a.K;
-#pragma unroll
-      for (int t = 0; t < T; ++t)
-        wv[t][s] = ok ? ld16_stream(wrow[t] + k) : make_uint4(0, 0, 0, 0);
-      xv[s] = (ok && mvalid) ? *reinterpret_cast<const uint4*>(xrow + k) : make_uint4(0, 0, 0, 0);
-    }
-    if (NORM) {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int64_t k = kb + s * 32;
-        float x[8], w[8];
-        unpack8(xv[s], x);
-        if (a.norm_w && k < a.K) {
-          unpack8(*reinterpret_cast<const uint4*>(a.norm_w + k), w);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) w[e] = 1.f;
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          ss = fmaf(x[e], x[e], ss);
-          x[e] *= w[e];
-        }
-        xv[s] = make_uint4(pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3]), pack_bf2(x[4], x[5]),
-                           pack_bf2(x[6], x[7]));
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const bf16x8_t bx = as_bf16x8(xv[s]);
-#pragma unroll
-      for (int t = 0; t < T; ++t)
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wv[t][s]), bx, acc[t], 0, 0, 0);
+  // Two fragment buffers: chunk c lives in buffer (c - cb) % 2 and its buffer
+  // is refilled with chunk c + 2 right after its MFMAs are issued.
+  MfmaFrag<T> fa, fb;
+  if (cb < ce) mfma_load<T, SILU>(fa, wrow, xrow, mvalid, chunk(cb), g, a.K);
+  if (cb + 1 < ce) mfma_load<T, SILU>(fb, wrow, xrow, mvalid, chunk(cb + 1), g, a.K);
+  for (int64_t c = cb; c < ce; c += 2) {
+    mfma_step<T>(acc, fa);
+    if (c + 2 < ce) mfma_load<T, SILU>(fa, wrow, xrow, mvalid, chunk(c + 2), g, a.K);
+    if (c + 1 < ce) {
+      mfma_step<T>(acc, fb);
+      if (c + 3 < ce) mfma_load<T, SILU>(fb, wrow, xrow, mvalid, chunk(c + 3), g, a.K);
     }
   }
 
@@ -231,31 +241,19 @@ __global__ __launch_bounds__(kBlock) void linear_mfma_kernel(LinearArgs a) {
   for (int t = 0; t < T; ++t)
 #pragma unroll
     for (int j = 0; j < 4; ++j) red[wave][t][j][lane] = acc[t][j];
-  if (NORM) {
-    ss += __shfl_xor(ss, 16, kWave);
-    ss += __shfl_xor(ss, 32, kWave);
-    if (g == 0) ssq[wave][i] = ss;
-  }
   __syncthreads();
 
   // Thread tid finalises output (j, l) = (tid / 64, tid % 64) of every tile.
   const int j = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int64_t mo = m0 + (l & 15);
   if (mo >= a.M) return;
-  float scale = 1.f;
-  if (NORM) {
-    float tot = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWavesPerBlock; ++w) tot += ssq[w][l & 15];
-    scale = rsqrtf(tot / float(a.K) + a.eps);
-  }
   float v[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     float sacc = 0.f;
 #pragma unroll
     for (int w = 0; w < kWavesPerBlock; ++w) sacc += red[w][t][j][l];
-    v[t] = sacc * scale;
+    v[t] = sacc;
   }
   const int rofs = 4 * (l >> 4) + j;
   if (SILU) {
@@ -267,6 +265,124 @@ __global__ __launch_bounds__(kBlock) void linear_mfma_kernel(LinearArgs a) {
       const int64_t n = tile0[t] + rofs;
       if (n < a.N) store_out(a, mo, n, v[t], 0.f);
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// LDS-staged MFMA skinny GEMM (M > 4).  The block owns T 16-row weight tiles
+// (T = 2: the gate and up tiles of the same rows) and streams K in 512-wide
+// chunks.  Weight rows are read with row-contiguous loads (a wave instruction
+// covers 4 rows x 256 B... in 16-byte pieces, 1 KiB of each row per chunk),
+// parked in registers while the previous chunk is multiplied, then written to
+// LDS, from where the MFMA fragments are read.  The 4 waves split each
+// chunk's 16 k-steps (wave w takes steps w, w+4, ...) and their partial tiles
+// are summed through LDS at the end.
+constexpr int kKC = 512;             // K elements per chunk
+constexpr int kRowPad = kKC + 8;     // LDS row stride in bf16 (16 B pad against bank conflicts)
+constexpr int kPieces = kKC / 8;     // 16-byte pieces per row per chunk
+
+template <int T>
+__global__ __launch_bounds__(kBlock) void linear_mfma_lds_kernel(LinearArgs a) {
+  constexpr bool SILU = T == 2;
+  constexpr int WROWS = 16 * T;
+  constexpr int WP = WROWS * kPieces / kBlock;  // weight pieces per thread per chunk
+  constexpr int XP = 16 * kPieces / kBlock;     // activation pieces per thread per chunk
+  __shared__ __align__(16) uint16_t Ws[WROWS][kRowPad];
+  __shared__ __align__(16) uint16_t Xs[16][kRowPad];
+  __shared__ float red[kWavesPerBlock][T][4][kWave];
+
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int i = lane & 15, g = lane >> 4;
+  const int64_t m0 = int64_t(blockIdx.y) * 16;
+  const int64_t n0 = int64_t(blockIdx.x) * (SILU ? 16 : WROWS);
+  const int64_t nchunks = (a.K + kKC - 1) / kKC;
+
+  // Row bases of the pieces this thread stages (piece p = u*kBlock + tid).
+  auto wsrc = [&](int u) -> const uint16_t* {
+    const int p = u * kBlock + tid, r = p / kPieces;
+    int64_t row = n0 + (SILU ? (r & 15) : r);
+    if (row >= a.N) row = a.N - 1;
+    return ((SILU && r >= 16) ? a.W2 : a.W) + row * a.K + (p % kPieces) * 8;
+  };
+  auto xsrc = [&](int u) -> const uint16_t* {
+    const int p = u * kBlock + tid, r = p / kPieces;
+    const int64_t m = m0 + r < a.M ? m0 + r : a.M - 1;
+    return a.X + m * a.ldx + (p % kPieces) * 8;
+  };
+
+  uint4 wr[WP], xr[XP];
+  auto fetch = [&](int64_t c) {
+    const int64_t k0 = c * kKC;
+#pragma unroll
+    for (int u = 0; u < WP; ++u) {
+      const int64_t k = k0 + ((u * kBlock + tid) % kPieces) * 8;
+      wr[u] = k < a.K ? ld16_stream(wsrc(u) + k0) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < XP; ++u) {
+      const int p = u * kBlock + tid;
+      const int64_t k = k0 + (p % kPieces) * 8;
+      xr[u] = (k < a.K && m0 + p / kPieces < a.M) ? *reinterpret_cast<const uint4*>(xsrc(u) + k0)
+                                                   : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto park = [&]() {
+#pragma unroll
+    for (int u = 0; u < WP; ++u) {
+      const int p = u * kBlock + tid;
+      *reinterpret_cast<uint4*>(&Ws[p / kPieces][(p % kPieces) * 8]) = wr[u];
+    }
+#pragma unroll
+    for (int u = 0; u < XP; ++u) {
+      const int p = u * kBlock + tid;
+      *reinterpret_cast<uint4*>(&Xs[p / kPieces][(p % kPieces) * 8]) = xr[u];
+    }
+  };
+
+  f32x4_t acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  if (nchunks > 0) fetch(0);
+  for (int64_t c = 0; c < nchunks; ++c) {
+    __syncthreads();  // previous chunk's fragments have been read
+    park();
+    __syncthreads();
+    if (c + 1 < nchunks) fetch(c + 1);  // next chunk streams while this one is multiplied
+#pragma unroll
+    for (int s = wave; s < kKC / 32; s += kWavesPerBlock) {
+      const bf16x8_t bx = as_bf16x8(*reinterpret_cast<const uint4*>(&Xs[i][32 * s + 8 * g]));
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            as_bf16x8(*reinterpret_cast<const uint4*>(&Ws[16 * t + i][32 * s + 8 * g])), bx, acc[t], 0, 0, 0);
+    }
+  }
+
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red[wave][t][j][lane] = acc[t][j];
+  __syncthreads();
+
+  const int j = tid >> 6, l = tid & 63;
+  const int64_t mo = m0 + (l & 15);
+  if (mo >= a.M) return;
+  float v[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    float sacc = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWavesPerBlock; ++w) sacc += red[w][t][j][l];
+    v[t] = sacc;
+  }
+  const int64_t n = n0 + 4 * (l >> 4) + j;
+  if (SILU) {
+    if (n < a.N) store_out(a, mo, n, v[0], v[1]);
+  } else {
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      if (n + 16 * t < a.N) store_out(a, mo, n + 16 * t, v[t], 0.f);
   }
 }
 
@@ -314,12 +430,22 @@ void launch_valu_m(const LinearArgs& a, hipStream_t s) {
   }
 }
 
-template <bool NORM, bool SILU>
+#ifndef EZ_MFMA_LDS
+#define EZ_MFMA_LDS 0  // 1: LDS-staged MFMA kernel for M > 4; 0: register-operand kernel
+#endif
+
+template <bool SILU>
 void launch_mfma(const LinearArgs& a, hipStream_t s) {
   constexpr int T = SILU ? 2 : 1;
   const int64_t blocks = SILU ? (a.N + 15) / 16 : (a.N + 16 * T - 1) / (16 * T);
   dim3 grid(unsigned(blocks), unsigned((a.M + 15) / 16));
-  hipLaunchKernelGGL((linear_mfma_kernel<T, NORM, SILU>), grid, dim3(kBlock), 0, s, a);
+  if (EZ_MFMA_LDS) {
+    const int64_t lblocks = (a.N + 15) / 16;  // one (or one gate+up pair of) 16-row tile(s) per block
+    dim3 lgrid(unsigned(lblocks), unsigned((a.M + 15) / 16));
+    hipLaunchKernelGGL((linear_mfma_lds_kernel<T>), lgrid, dim3(kBlock), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((linear_mfma_kernel<T, SILU>), grid, dim3(kBlock), 0, s, a);
+  }
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -346,11 +472,19 @@ int launch_linear(const LinearArgs& a, hipStream_t s) {
       silu ? launch_valu_m<false, true>(a, s) : launch_valu_m<false, false>(a, s);
     }
   } else {
+    // M > 4: the RMSNorm'd input is staged once as bf16(x * rsqrt(mean x^2 +
+    // eps) * w) (the reference's staging) into the caller's workspace, then
+    // a plain MFMA GEMM runs on it.
+    LinearArgs b = a;
     if (a.norm) {
-      silu ? launch_mfma<true, true>(a, s) : launch_mfma<true, false>(a, s);
-    } else {
-      silu ? launch_mfma<false, true>(a, s) : launch_mfma<false, false>(a, s);
+      EZ_REQUIRE(a.xn_ws, "linear: RMSNorm prologue with M > 4 needs a workspace of M*K bf16");
+      EZ_REQUIRE(a.ldx == a.K, "linear: RMSNorm prologue with M > 4 needs contiguous X rows");
+      const int rc = ezops_rmsnorm_bf16(a.X, a.norm_w, a.xn_ws, a.M, a.K, a.eps, s);
+      if (rc) return rc;
+      b.X = a.xn_ws;
+      b.norm = 0;
     }
+    silu ? launch_mfma<true>(b, s) : launch_mfma<false>(b, s);
   }
   return launch_status("linear");
 }
@@ -388,10 +522,15 @@ extern "C" int ezops_linear_bf16(const void* X, int64_t ldx, const void* W, void
   return ez::launch_linear(a, stream);
 }
 
+extern "C" size_t ezops_linear_stage_workspace_size(int64_t M, int64_t K, int norm) {
+  return (norm && M > 4) ? size_t(M * K) * 2 : 0;
+}
+
 extern "C" int ezops_linear_stage_bf16(const void* X, int64_t ldx, const void* W, const void* W2, void* Y,
                                        int64_t ldy, const void* res, int64_t ldr, const void* norm_w, int norm,
-                                       float eps, int epilogue, int64_t M, int64_t N, int64_t K,
-                                       hipStream_t stream) {
+                                       float eps, int epilogue, int64_t M, int64_t N, int64_t K, void* workspace,
+                                       size_t workspace_bytes, hipStream_t stream) {
+  EZ_REQUIRE(workspace_bytes >= ezops_linear_stage_workspace_size(M, K, norm), "linear_stage: workspace too small");
   EZ_REQUIRE(epilogue >= ez::kEpiStore && epilogue <= ez::kEpiStoreF32, "linear_stage: epilogue must be 0..3");
   EZ_REQUIRE(ldx >= K && ldy >= N && (epilogue != ez::kEpiResid || ldr >= N),
              "linear_stage: leading dimensions too small");
@@ -411,5 +550,6 @@ extern "C" int ezops_linear_stage_bf16(const void* X, int64_t ldx, const void* W
   a.norm_w = static_cast<const uint16_t*>(norm_w);
   a.eps = eps;
   a.epi = epilogue;
+  a.xn_ws = static_cast<uint16_t*>(workspace);
   return ez::launch_linear(a, stream);
 }

@@ -29,6 +29,7 @@ struct LinearArgs {
   const uint16_t* norm_w;      // NULL = unit weight
   float eps;
   int epi;
+  uint16_t* xn_ws;             // M > 4 with `norm`: M*K bf16 scratch for the staged input
 };
 
 int launch_linear(const LinearArgs& a, hipStream_t s);

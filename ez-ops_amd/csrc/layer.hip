@@ -399,7 +399,7 @@ __global__ __launch_bounds__(kLThreads) void qwen3_layer_persistent(LayerArgs p)
     a.out_f = p.attn_f;
     const int64_t items = p.B * p.Hkv * p.nsplit;
     for (int64_t it = blockIdx.x; it < items; it += nb) {
-      attn::attn_block<128, G, kLWaves, attn::kQFromQkvF32, attn::kOutF32Dev>(a, it % p.nsplit, it / p.nsplit,
+      attn::attn_block<128, G, kLWaves, attn::kQFromQkvF32, attn::kOutF32Dev, true>(a, it % p.nsplit, it / p.nsplit,
                                                                              p.nsplit, p.chunk, p.aws);
       __syncthreads();
     }

@@ -40,8 +40,9 @@ SIGNATURES: dict[str, tuple] = {
     "ezops_hip_last_error": (C.c_char_p, []),
     "ezops_gemv_bf16": (_i32, [_p, _p, _p, _i64, _i64, _p]),
     "ezops_linear_bf16": (_i32, [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p]),
+    "ezops_linear_stage_workspace_size": (_sz, [_i64, _i64, _i32]),
     "ezops_linear_stage_bf16": (_i32, [_p, _i64, _p, _p, _p, _i64, _p, _i64, _p, _i32, _f32, _i32, _i64, _i64,
-                                       _i64, _p]),
+                                       _i64, _p, _sz, _p]),
     "ezops_rmsnorm_f32": (_i32, [_p, _p, _i64, _i64, _f32, _p]),
     "ezops_rmsnorm_bf16": (_i32, [_p, _p, _p, _i64, _i64, _f32, _p]),
     "ezops_softmax_f32": (_i32, [_p, _p, _i64, _i64, _p]),

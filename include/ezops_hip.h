@@ -59,14 +59,16 @@ int ezops_linear_bf16(const void* X, int64_t ldx, const void* W, void* Y, int64_
  * Xn = X, or with norm != 0, Xn = X * rsqrt(mean(X^2) + eps) * norm_w
  * (norm_w NULL = unit).  epilogue 0: Y = bf16(acc); 1: Y = bf16(res + bf16(acc));
  * 2: SwiGLU, W2 holds the up rows: Y = bf16(bf16(silu(bf16(g))) * bf16(u));
- * 3: Y = acc as fp32.
+ * 3: Y = acc as fp32.  With norm and M > 4 the normalised input is staged in
+ * the workspace (ezops_linear_stage_workspace_size bytes; X rows contiguous).
  * Replaces: the per-stage kernels of the reference's multi-launch fused
  * variants (ezops/kernels/fused_o_proj_ffn/fused_o_proj_ffn_tl.py:49-250,
  * ezops/kernels/qwen3_dense_decode/qwen3_dense_decode_multilaunch_tl.py:68-588). */
+size_t ezops_linear_stage_workspace_size(int64_t M, int64_t K, int norm);
 int ezops_linear_stage_bf16(const void* X, int64_t ldx, const void* W, const void* W2, void* Y,
                             int64_t ldy, const void* res, int64_t ldr, const void* norm_w, int norm,
-                            float eps, int epilogue, int64_t M, int64_t N, int64_t K,
-                            hipStream_t stream);
+                            float eps, int epilogue, int64_t M, int64_t N, int64_t K, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream);
 
 /* fp32 RMSNorm without weight: Out = X * rsqrt(mean(X^2) + eps), per row.
  * X, Out [rows, dim].

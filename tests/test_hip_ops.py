@@ -236,3 +236,35 @@ def test_golden_qk_norm_rope_through_abi(golden):
     for b, p in enumerate(gd["rope_pos"]):
         np.testing.assert_array_equal(n(Vc)[b, :, p], gd["rope_v"][b])
         np.testing.assert_array_equal(n(Kc)[b, :, p], n(ko)[b])
+
+
+@pytest.mark.parametrize("M", [1, 3, 8, 16])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3])
+@pytest.mark.parametrize("norm", [0, 1])
+def test_linear_stage_epilogues(M, epi, norm):
+    """ezops_linear_stage_bf16: RMSNorm prologue x epilogues, VALU (M <= 4) and MFMA (M > 4) paths."""
+    rng = np.random.default_rng(100 * M + 10 * epi + norm)
+    N, K = 192, 512
+    X = oracle.bf16(rng.standard_normal((M, K)).astype(np.float32))
+    W = oracle.bf16(rng.standard_normal((N, K)).astype(np.float32) * K ** -0.5)
+    W2 = oracle.bf16(rng.standard_normal((N, K)).astype(np.float32) * K ** -0.5)
+    R = oracle.bf16(rng.standard_normal((M, N)).astype(np.float32))
+    w = oracle.bf16(rng.standard_normal(K).astype(np.float32) * 0.1 + 1)
+    Xn = oracle.rmsnorm_bf16(X, w) if norm else X
+    g_ = oracle.linear_bf16(Xn, W)
+    if epi == 0:
+        ref = g_
+    elif epi == 1:
+        ref = oracle.bf16(R + g_)
+    elif epi == 2:
+        u = oracle.linear_bf16(Xn, W2)
+        ref = oracle.bf16(oracle.bf16(g_ / (1 + np.exp(-g_.astype(np.float64)))) * u)
+    else:
+        ref = Xn @ W.T
+    tX, tW, tW2, tR, tw = g(X), g(W), g(W2), g(R), g(w)
+    Y = torch.empty(M, N, dtype=torch.float32 if epi == 3 else torch.bfloat16, device=DEV)
+    ws = torch.zeros(max(256, _hip.size("ezops_linear_stage_workspace_size", M, K, norm)), dtype=torch.uint8,
+                     device=DEV)
+    _hip.call("ezops_linear_stage_bf16", tX.data_ptr(), K, tW.data_ptr(), tW2.data_ptr(), Y.data_ptr(), N,
+              tR.data_ptr(), N, tw.data_ptr(), norm, 1e-6, epi, M, N, K, ws.data_ptr(), ws.numel(), _hip.stream())
+    np.testing.assert_allclose(n(Y), ref, rtol=2e-2, atol=3e-2)
