@@ -24,9 +24,12 @@ int num_cus() {
 
 struct SplitPlan {
   int waves;
-  int64_t nsplit, chunk;
+  int64_t nsplit;
 };
 
+// Splits per (b, kv head), planned on the cache capacity S: enough blocks to
+// keep every CU busy, at least one tile per wave at full capacity, and at
+// most kMaxSplits partials per merge.
 SplitPlan plan_splits(int64_t B, int64_t Hkv, int64_t S, int64_t G) {
   const int64_t units = B * Hkv;
   const int64_t cus = num_cus();
@@ -35,24 +38,24 @@ SplitPlan plan_splits(int64_t B, int64_t Hkv, int64_t S, int64_t G) {
   const int waves = (units * 4 <= cus && G <= 4) ? 8 : 4;
   const int64_t target = waves == 8 ? 2 * cus : 8 * cus;  // blocks in flight
   int64_t ns = (target + units - 1) / units;
-  const int64_t min_chunk = int64_t(waves) * kTile;
-  const int64_t max_ns = (S + min_chunk - 1) / min_chunk;
+  const int64_t max_ns = (S + int64_t(waves) * kTile - 1) / (int64_t(waves) * kTile);
   if (ns > max_ns) ns = max_ns;
   if (ns > kMaxSplits) ns = kMaxSplits;
   if (ns < 1) ns = 1;
-  int64_t chunk = (S + ns - 1) / ns;
-  chunk = (chunk + kTile - 1) / kTile * kTile;
-  ns = (S + chunk - 1) / chunk;
-  return {waves, ns, chunk};
+  return {waves, ns};
 }
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
+#ifndef EZ_ATTN_MERGE_LAST
+#define EZ_ATTN_MERGE_LAST 0  // 1: the last block of a unit merges its splits (no combine launch)
+#endif
+constexpr bool kMergeLast = EZ_ATTN_MERGE_LAST;
+
 template <int D, int G, int W, int QSRC>
-__global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int64_t nsplit, int64_t chunk,
-                                                               AttnWs ws) {
-  attn::attn_block<D, G, W, QSRC, attn::kOutBf16, false>(a, blockIdx.x % nsplit, blockIdx.x / nsplit, nsplit, chunk,
-                                                        ws);
+__global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int64_t nsplit, AttnWs ws) {
+  attn::attn_block<D, G, W, QSRC, attn::kOutBf16, kMergeLast>(a, blockIdx.x % nsplit, blockIdx.x / nsplit, nsplit,
+                                                              ws);
 }
 
 // One wave per query head merges that head's split partials.
@@ -65,9 +68,9 @@ template <int D, int W, int LAYER>
 void launch_dw(const AttnArgs& a, const SplitPlan& pl, const AttnWs& ws, int64_t G, hipStream_t s) {
   const dim3 grid{unsigned(a.B * a.Hkv * pl.nsplit), 1, 1}, block{unsigned(W * kWave), 1, 1};
   switch (G) {
-    case 1: hipLaunchKernelGGL((attn_split_kernel<D, 1, W, LAYER>), grid, block, 0, s, a, pl.nsplit, pl.chunk, ws); break;
-    case 2: hipLaunchKernelGGL((attn_split_kernel<D, 2, W, LAYER>), grid, block, 0, s, a, pl.nsplit, pl.chunk, ws); break;
-    case 4: hipLaunchKernelGGL((attn_split_kernel<D, 4, W, LAYER>), grid, block, 0, s, a, pl.nsplit, pl.chunk, ws); break;
+    case 1: hipLaunchKernelGGL((attn_split_kernel<D, 1, W, LAYER>), grid, block, 0, s, a, pl.nsplit, ws); break;
+    case 2: hipLaunchKernelGGL((attn_split_kernel<D, 2, W, LAYER>), grid, block, 0, s, a, pl.nsplit, ws); break;
+    case 4: hipLaunchKernelGGL((attn_split_kernel<D, 4, W, LAYER>), grid, block, 0, s, a, pl.nsplit, ws); break;
     default: break;  // group 8 launches from launch_d
   }
 }
@@ -77,7 +80,7 @@ void launch_d(const AttnArgs& a, const SplitPlan& pl, const AttnWs& ws, int64_t 
   const dim3 block{unsigned(pl.waves * kWave), 1, 1};
   const dim3 grid{unsigned(a.B * a.Hkv * pl.nsplit), 1, 1};
   if (G == 8) {
-    hipLaunchKernelGGL((attn_split_kernel<D, 8, 4, LAYER>), grid, block, 0, s, a, pl.nsplit, pl.chunk, ws);
+    hipLaunchKernelGGL((attn_split_kernel<D, 8, 4, LAYER>), grid, block, 0, s, a, pl.nsplit, ws);
   } else if (pl.waves == 8) {
     launch_dw<D, 8, LAYER>(a, pl, ws, G, s);
   } else {
@@ -125,7 +128,7 @@ int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
     if (a.D == 64) launch_d<64, attn::kQFromQ>(aa, pl, w, G, s);
     else launch_d<128, attn::kQFromQ>(aa, pl, w, G, s);
   }
-  if (pl.nsplit > 1) {
+  if (pl.nsplit > 1 && !kMergeLast) {
     const dim3 grid{unsigned(a.B * a.H), 1, 1}, block{kWave, 1, 1};
     if (a.D == 64) hipLaunchKernelGGL(attn_combine_kernel<64>, grid, block, 0, s, aa, pl.nsplit, w);
     else hipLaunchKernelGGL(attn_combine_kernel<128>, grid, block, 0, s, aa, pl.nsplit, w);

@@ -1,10 +1,15 @@
 // Split-KV GQA decode attention: the per-block device routine, shared by the
 // standalone kernel (attn.hip) and the persistent layer kernel (layer.hip).
 //
-// Work unit = (sequence b, kv head, split).  One block of W waves owns a
-// contiguous chunk of KV positions of one (b, kv head); its G = H / Hkv query
-// heads share every K/V byte it loads, so K/V cross HBM once per GQA group.
-// Each wave walks 32-position tiles:
+// Work unit = (sequence b, kv head, split).  One block of W waves serves one
+// (b, kv head); its G = H / Hkv query heads share every K/V byte it loads, so
+// K/V cross HBM once per GQA group.  The 32-position tiles of the sequence
+// are dealt round-robin: wave w of split s takes tiles s*W + w,
+// s*W + w + nsplit*W, ...  The split count is planned on the cache capacity
+// (the live lengths are on the device), and the round-robin deal spreads any
+// live length evenly over all blocks and waves; the first tile's address does
+// not depend on the length, so it is requested before the length arrives.
+// Each wave walks its tiles:
 //   * scores S[h, p] = q_h . k_p on MFMA (v_mfma_f32_16x16x32_bf16): A = the
 //     G query rows (zero-padded to 16), B = 16 positions of K per sub-tile;
 //     lanes load 16-byte pieces of K rows straight into the B operand.
@@ -33,7 +38,13 @@ namespace attn {
 
 constexpr int kTile = EZ_ATTN_TILE;  // positions per wave iteration
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kMaxSplits = 32;       // split partials a merge thread loads at once
+#ifndef EZ_ATTN_SPEC
+#define EZ_ATTN_SPEC 1  // request the first tile before the sequence length is known
+#endif
+#ifndef EZ_ATTN_MAX_SPLITS
+#define EZ_ATTN_MAX_SPLITS 32
+#endif
+constexpr int kMaxSplits = EZ_ATTN_MAX_SPLITS;  // split partials a merge thread loads at once
 
 struct AttnWs {
   float* opart;   // [B, H, nsplit, D]
@@ -132,7 +143,7 @@ __device__ __forceinline__ void norm_rope_head(const T* src, const uint16_t* w, 
 // cheaper than the in-kernel store -> wait -> count -> load chain).
 template <int D, int G, int W, int QSRC, int OUT, bool MERGE_LAST>
 __device__ __forceinline__ void attn_block(const AttnArgs& a, int64_t split, int64_t unit, int64_t nsplit,
-                                           int64_t chunk, const AttnWs& ws) {
+                                           const AttnWs& ws) {
   constexpr bool LAYER = QSRC != kQFromQ;
   constexpr int NT = W * kWave;      // threads per block
   constexpr int NS = D / 32;         // MFMA k-steps per 16-position sub-tile
@@ -157,28 +168,31 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, int64_t split, int
   const int64_t h0 = kvh * G;  // first query head of the group
   const float sl2 = a.scale * kLog2e;
   const int dc = lane % CPR, rs = lane / CPR;
-  const int64_t p_begin = split * chunk;
+  const int64_t stride = nsplit * W * kTile;  // distance between a wave's tiles
 
   // The first tile is requested before the sequence length arrives: its
   // addresses only need the cache capacity (clamped to slot S-1), and rows at
   // or beyond the real length are masked below (scores to -inf, V rows to 0).
-  int64_t t0 = p_begin + int64_t(wave) * kTile;
-  const int64_t spec_end = (p_begin + chunk < a.S) ? p_begin + chunk : a.S;
+  int64_t t0 = (split * W + wave) * kTile;
   uint4 kf[NSUB][NS], vf[NPV];
-  if (t0 < spec_end) {
-    load_k_tile<D, NSUB>(Kb, t0, spec_end - 1, li, lg, kf);
-    load_v_tile<D, NPV>(Vb, t0, spec_end - 1, dc, rs, vf);
+  if (EZ_ATTN_SPEC && t0 < a.S) {
+    load_k_tile<D, NSUB>(Kb, t0, a.S - 1, li, lg, kf);
+    load_v_tile<D, NPV>(Vb, t0, a.S - 1, dc, rs, vf);
   }
 
   int64_t L = a.kv_lens ? int64_t(a.kv_lens[b]) : a.S;
   L = L < 0 ? 0 : (L > a.S ? a.S : L);
-  const int64_t p_end = (p_begin + chunk < L) ? p_begin + chunk : L;
+  const int64_t p_end = L;
   const int64_t last = p_end - 1;
+  if (!EZ_ATTN_SPEC && t0 < p_end) {
+    load_k_tile<D, NSUB>(Kb, t0, last, li, lg, kf);
+    load_v_tile<D, NPV>(Vb, t0, last, dc, rs, vf);
+  }
 
-  // The block whose chunk holds the decoded token writes its k/v slot and
-  // then reloads its first tile, which may have been read before the write.
+  // The block dealt the tile that holds the decoded token writes its k/v
+  // slot; the wave whose first (already requested) tile holds it reloads it.
   const int64_t pos = L - 1;
-  const bool owner = LAYER && pos >= p_begin && pos < p_end;
+  const bool owner = LAYER && L > 0 && ((pos / kTile) / W) % nsplit == split;
 
   bf16x8_t qf[NS];
   if constexpr (LAYER) {
@@ -203,9 +217,9 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, int64_t split, int
       }
     }
     __syncthreads();  // Qs complete; the cache slot written by this block is visible to it
-    if (owner && t0 < p_end) {
-      load_k_tile<D, NSUB>(Kb, t0, spec_end - 1, li, lg, kf);
-      load_v_tile<D, NPV>(Vb, t0, spec_end - 1, dc, rs, vf);
+    if (owner && t0 <= pos && pos < t0 + kTile) {
+      load_k_tile<D, NSUB>(Kb, t0, a.S - 1, li, lg, kf);
+      load_v_tile<D, NPV>(Vb, t0, a.S - 1, dc, rs, vf);
     }
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
@@ -232,8 +246,8 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, int64_t split, int
     for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
   }
 
-  for (; t0 < p_end; t0 += int64_t(W) * kTile) {
-    const int64_t tn = t0 + int64_t(W) * kTile;
+  for (; t0 < p_end; t0 += stride) {
+    const int64_t tn = t0 + stride;
     // ---- scores: acc[u][j] = S[head 4*lg + j][pos t0 + 16u + li]
     f32x4_t acc[NSUB];
 #pragma unroll

@@ -72,7 +72,7 @@ struct LayerArgs {
   float* x2_f;    // [B, HS]
   float* h_f;     // [B, IS]
   attn::AttnWs aws;
-  int64_t nsplit, chunk;
+  int64_t nsplit;
   GridBar* bar;
 };
 
@@ -400,7 +400,7 @@ __global__ __launch_bounds__(kLThreads) void qwen3_layer_persistent(LayerArgs p)
     const int64_t items = p.B * p.Hkv * p.nsplit;
     for (int64_t it = blockIdx.x; it < items; it += nb) {
       attn::attn_block<128, G, kLWaves, attn::kQFromQkvF32, attn::kOutF32Dev, true>(a, it % p.nsplit, it / p.nsplit,
-                                                                             p.nsplit, p.chunk, p.aws);
+                                                                             p.nsplit, p.aws);
       __syncthreads();
     }
   }
@@ -456,7 +456,7 @@ int grid_blocks() {
 }
 
 struct MkPlan {
-  int64_t nsplit, chunk;
+  int64_t nsplit;
 };
 
 MkPlan mk_plan(const ezops_qwen3_layer& L) {
@@ -467,10 +467,7 @@ MkPlan mk_plan(const ezops_qwen3_layer& L) {
   if (ns > max_ns) ns = max_ns;
   if (ns > attn::kMaxSplits) ns = attn::kMaxSplits;
   if (ns < 1) ns = 1;
-  int64_t chunk = (L.S + ns - 1) / ns;
-  chunk = (chunk + attn::kTile - 1) / attn::kTile * attn::kTile;
-  ns = (L.S + chunk - 1) / chunk;
-  return {ns, chunk};
+  return {ns};
 }
 
 template <int M, int G>
@@ -542,7 +539,6 @@ int launch_layer_persistent(const ezops_qwen3_layer& L, void* ws, hipStream_t s)
   p.out = static_cast<uint16_t*>(L.out);
   const MkPlan pl = mk_plan(L);
   p.nsplit = pl.nsplit;
-  p.chunk = pl.chunk;
   char* c = static_cast<char*>(ws);
   auto take = [&](size_t bytes) {
     char* r = c;

@@ -172,8 +172,9 @@ int ezops_qwen3_dense_decode_bf16(const ezops_qwen3_layer* p, void* workspace,
 
 /* STREAM-style HBM probes used to measure the chip's bandwidth peak
  * (replaces benchmarks/hardware/memory/hbm_saturation.cu:49-90):
- * kind 0 = read (sum into out[0..]), 1 = write, 2 = copy, 3 = triad
- * a = b + s*c.  n = float count per array. */
+ * kind 0 = read (sum into out[0..]; allocates in the caches, used as the
+ * cache flush), 1 = write, 2 = copy, 3 = triad a = b + s*c, 4 = streaming read
+ * (non-temporal hint).  n = float count per array. */
 int ezops_hbm_probe(int kind, float* a, const float* b, const float* c, int64_t n, float s,
                     hipStream_t stream);
 
