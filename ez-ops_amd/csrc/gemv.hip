@@ -37,6 +37,9 @@ constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
 constexpr int kGemvBlock = EZ_GEMV_BLOCK;
 constexpr int kGemvWaves = kGemvBlock / kWave;
+#ifndef EZ_GEMV_RES_PREFETCH
+#define EZ_GEMV_RES_PREFETCH 1
+#endif
 
 __device__ __forceinline__ void store_out(const LinearArgs& a, int64_t m, int64_t n, float v,
                                           float v_up) {
@@ -79,6 +82,17 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_valu_kernel(LinearArgs a) {
 #pragma unroll
   for (int m = 0; m < M; ++m) xp[m] = reinterpret_cast<const uint4*>(a.X + m * a.ldx);
   const uint4* nwp = reinterpret_cast<const uint4*>(a.norm_w);
+
+  // The residual is requested with the first weight loads, so the epilogue
+  // does not wait on a cold load after the reduction.
+  float resv[M][R];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t n = SILU ? n0 : (n0 + r < a.N ? n0 + r : a.N - 1);
+      resv[m][r] = (EZ_GEMV_RES_PREFETCH && a.epi == kEpiResid) ? bf2f(a.res[m * a.ldr + n]) : 0.f;
+    }
 
   float acc[M][R];
   float ss[M];
@@ -139,8 +153,13 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_valu_kernel(LinearArgs a) {
         store_out(a, m, n0, v[0], v[1]);
       } else {
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-          if (n0 + r < a.N) store_out(a, m, n0 + r, v[r], 0.f);
+        for (int r = 0; r < R; ++r) {
+          if (n0 + r >= a.N) continue;
+          if (EZ_GEMV_RES_PREFETCH && a.epi == kEpiResid)
+            reinterpret_cast<uint16_t*>(a.Y)[m * a.ldy + n0 + r] = f2bf(resv[m][r] + round_bf(v[r]));
+          else
+            store_out(a, m, n0 + r, v[r], 0.f);
+        }
       }
     }
   }
@@ -265,6 +284,121 @@ __global__ __launch_bounds__(kBlock) void linear_mfma_kernel(LinearArgs a) {
       const int64_t n = tile0[t] + rofs;
       if (n < a.N) store_out(a, mo, n, v[t], 0.f);
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Row-block GEMV, M <= 4 and K = 2048 * CH.  A block of 256 threads owns RB
+// output rows (SwiGLU: RB gate rows and the RB matching up rows); thread t
+// holds the 16-byte chunks t, t + 256, ... of every row, so each wave
+// instruction reads 1 KiB of one row, all weight loads of a thread are issued
+// back to back with no bounds branches, and every x chunk a thread loads
+// serves all RB rows (x traffic through L2 is 1/RB of the weight traffic).
+// Partial sums are reduced per wave (DPP) and across the 4 waves through LDS.
+template <int M, int RB, int CH, bool NORM, bool SILU>
+__global__ __launch_bounds__(kBlock) void gemv_rows_kernel(LinearArgs a) {
+  constexpr int NR = SILU ? 2 * RB : RB;  // weight rows per block
+  constexpr int NQ = M * NR + (NORM ? M : 0);
+  __shared__ float red[kWavesPerBlock][NQ];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int64_t n0 = int64_t(blockIdx.x) * RB;
+
+  uint4 wv[NR][CH];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const uint16_t* base = (SILU && r >= RB) ? a.W2 : a.W;
+    int64_t row = n0 + (r % RB);
+    if (row >= a.N) row = a.N - 1;  // tail rows: load a valid row, skip the store
+    const uint4* wp = reinterpret_cast<const uint4*>(base + row * a.K) + tid;
+#pragma unroll
+    for (int j = 0; j < CH; ++j) wv[r][j] = ld16_stream(wp + kBlock * j);
+  }
+  uint4 xv[M][CH];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int j = 0; j < CH; ++j) xv[m][j] = reinterpret_cast<const uint4*>(a.X + m * a.ldx)[tid + kBlock * j];
+  uint4 nv[NORM ? CH : 1];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int j = 0; j < CH; ++j)
+      nv[j] = a.norm_w ? reinterpret_cast<const uint4*>(a.norm_w)[tid + kBlock * j]
+                       : make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
+  }
+  // The finishing thread (m, r) fetches its residual with the weight loads.
+  uint16_t res_raw = 0;
+  if (a.epi == kEpiResid && tid < M * RB) {
+    const int64_t n = n0 + tid % RB;
+    if (n < a.N) res_raw = a.res[(tid / RB) * a.ldr + n];
+  }
+
+  float acc[M][NR], ss[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    ss[m] = 0.f;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) acc[m][r] = 0.f;
+  }
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    float nw[8];
+    if constexpr (NORM) unpack8(nv[j], nw);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float x[8];
+      unpack8(xv[m][j], x);
+      if constexpr (NORM) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          ss[m] = fmaf(x[e], x[e], ss[m]);
+          x[e] *= nw[e];
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        float w[8];
+        unpack8(wv[r][j], w);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[m][r] = fmaf(w[e], x[e], acc[m][r]);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const float v = wave_reduce_uniform<false>(acc[m][r]);
+      if (lane == 0) red[wave][m * NR + r] = v;
+    }
+    if constexpr (NORM) {
+      const float v = wave_reduce_uniform<false>(ss[m]);
+      if (lane == 0) red[wave][M * NR + m] = v;
+    }
+  }
+  __syncthreads();
+  if (tid >= M * RB) return;
+  const int m = tid / RB, r = tid % RB;
+  const int64_t n = n0 + r;
+  if (n >= a.N) return;
+  float v = 0.f, vu = 0.f, scale = 1.f;
+#pragma unroll
+  for (int w = 0; w < kWavesPerBlock; ++w) {
+    v += red[w][m * NR + r];
+    if constexpr (SILU) vu += red[w][m * NR + RB + r];
+  }
+  if constexpr (NORM) {
+    float sq = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWavesPerBlock; ++w) sq += red[w][M * NR + m];
+    scale = rsqrtf(sq / float(a.K) + a.eps);
+  }
+  v *= scale;
+  vu *= scale;
+  if (a.epi == kEpiResid) {
+    reinterpret_cast<uint16_t*>(a.Y)[m * a.ldy + n] = f2bf(bf2f(res_raw) + round_bf(v));
+  } else {
+    store_out(a, m, n, v, vu);
   }
 }
 
@@ -420,8 +554,41 @@ void launch_valu(const LinearArgs& a, hipStream_t s) {
   hipLaunchKernelGGL((gemv_valu_kernel<M, R, U, NORM, SILU>), dim3(blocks), dim3(kGemvBlock), 0, s, a);
 }
 
+#ifndef EZ_ROWS_RB4K
+#define EZ_ROWS_RB4K 4   // rows per block of the row-block GEMV at K = 4096 (SwiGLU: half)
+#endif
+#ifndef EZ_ROWS_RB12K
+#define EZ_ROWS_RB12K 2  // rows per block at K = 12288
+#endif
+#ifndef EZ_GEMV_ROWS
+#define EZ_GEMV_ROWS 1   // 0: always the wave-per-row kernel
+#endif
+
+template <int M, int CH, bool NORM, bool SILU>
+void launch_rows(const LinearArgs& a, hipStream_t s) {
+  constexpr int RB0 = CH <= 2 ? EZ_ROWS_RB4K : EZ_ROWS_RB12K;
+  constexpr int RB = SILU ? (RB0 / 2 > 0 ? RB0 / 2 : 1) : RB0;
+  const int64_t blocks = (a.N + RB - 1) / RB;
+  hipLaunchKernelGGL((gemv_rows_kernel<M, RB, CH, NORM, SILU>), dim3(unsigned(blocks)), dim3(kBlock), 0, s, a);
+}
+
+template <int CH, bool NORM, bool SILU>
+void launch_rows_m(const LinearArgs& a, hipStream_t s) {
+  switch (a.M) {
+    case 1: launch_rows<1, CH, NORM, SILU>(a, s); break;
+    case 2: launch_rows<2, CH, NORM, SILU>(a, s); break;
+    case 3: launch_rows<3, CH, NORM, SILU>(a, s); break;
+    default: launch_rows<4, CH, NORM, SILU>(a, s); break;
+  }
+}
+
 template <bool NORM, bool SILU>
 void launch_valu_m(const LinearArgs& a, hipStream_t s) {
+  if (EZ_GEMV_ROWS && a.ldx % 8 == 0 && (a.K == 4096 || a.K == 12288)) {
+    if (a.K == 4096) launch_rows_m<2, NORM, SILU>(a, s);
+    else launch_rows_m<6, NORM, SILU>(a, s);
+    return;
+  }
   switch (a.M) {
     case 1: launch_valu<1, NORM, SILU>(a, s); break;
     case 2: launch_valu<2, NORM, SILU>(a, s); break;
