@@ -38,6 +38,9 @@ namespace attn {
 
 constexpr int kTile = EZ_ATTN_TILE;  // positions per wave iteration
 constexpr float kLog2e = 1.4426950408889634f;
+#ifndef EZ_ATTN_XP
+#define EZ_ATTN_XP 0  // timing experiments only
+#endif
 #ifndef EZ_ATTN_SPEC
 #define EZ_ATTN_SPEC 1  // request the first tile before the sequence length is known
 #endif
@@ -246,6 +249,19 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, int64_t split, int
     for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
   }
 
+#if EZ_ATTN_XP == 1
+  {
+    unsigned x = 0;
+    for (; t0 < p_end; t0 += stride) {
+      for (int u = 0; u < NSUB; ++u) for (int s = 0; s < NS; ++s) x ^= kf[u][s].x ^ kf[u][s].w;
+      for (int j = 0; j < NPV; ++j) x ^= vf[j].y ^ vf[j].z;
+      const int64_t tn = t0 + stride;
+      if (tn < p_end) { load_k_tile<D, NSUB>(Kb, tn, last, li, lg, kf); load_v_tile<D, NPV>(Vb, tn, last, dc, rs, vf); }
+    }
+    if (x == 0x12345u) a.Out[0] = 1;
+    return;
+  }
+#endif
   for (; t0 < p_end; t0 += stride) {
     const int64_t tn = t0 + stride;
     // ---- scores: acc[u][j] = S[head 4*lg + j][pos t0 + 16u + li]
@@ -329,6 +345,27 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, int64_t split, int
     __builtin_amdgcn_wave_barrier();
   }
 
+#if EZ_ATTN_XP == 2
+  {
+    float z = 0.f;
+    for (int h = 0; h < G; ++h) { z += l_acc[h] + m_run[h]; for (int e = 0; e < 8; ++e) z += o[h][e]; }
+    if (z == 12345.f) a.Out[0] = 1;
+    return;
+  }
+#endif
+#if EZ_ATTN_XP == 3
+  {  // in-wave merge only
+    for (int h = 0; h < G; ++h)
+      for (int off = CPR; off < kWave; off <<= 1) {
+        l_acc[h] += __shfl_xor(l_acc[h], off, kWave);
+        for (int e = 0; e < 8; ++e) o[h][e] += __shfl_xor(o[h][e], off, kWave);
+      }
+    float z = 0.f;
+    for (int h = 0; h < G; ++h) { z += l_acc[h] + m_run[h]; for (int e = 0; e < 8; ++e) z += o[h][e]; }
+    if (z == 12345.f) a.Out[0] = 1;
+    return;
+  }
+#endif
   // ---- merge the row groups of the wave (lanes with equal dc)
 #pragma unroll
   for (int h = 0; h < G; ++h) {

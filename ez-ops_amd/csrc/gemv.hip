@@ -178,30 +178,50 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_valu_kernel(LinearArgs a) {
 // of a 128-wide chunk) is the same for A and B, so the contraction is
 // exact, and each wave load instruction reads 64 contiguous bytes (4 lanes)
 // of each of its 16 weight rows.
+#ifndef EZ_MFMA_XP
+#define EZ_MFMA_XP 0  // timing experiments only
+#endif
+#ifndef EZ_MFMA_T1
+#define EZ_MFMA_T1 1  // 16-row weight tiles per wave (sharing each X fragment), plain epilogues
+#endif
+#ifndef EZ_MFMA_WAVES
+#define EZ_MFMA_WAVES 8   // waves per block of the MFMA kernel (the K range is split over them)
+#endif
+#ifndef EZ_MFMA_STEPS
+#define EZ_MFMA_STEPS 8   // 32-wide k-steps per fragment buffer (two buffers in flight)
+#endif
+constexpr int kMfmaWaves = EZ_MFMA_WAVES;
+constexpr int kMfmaSteps = EZ_MFMA_STEPS;
+constexpr int kMfmaChunk = 32 * kMfmaSteps;
+
 template <int T>
 struct MfmaFrag {
-  uint4 w[T][4];
-  uint4 x[4];
+  uint4 w[T][kMfmaSteps];
+  uint4 x[kMfmaSteps];
 };
 
 template <int T, bool SILU>
 __device__ __forceinline__ void mfma_load(MfmaFrag<T>& f, const uint16_t* const (&wrow)[T], const uint16_t* xrow,
                                           bool mvalid, int64_t c, int g, int64_t K) {
-  const int64_t kb = c * 128 + g * 8;
+  const int64_t kb = c * kMfmaChunk + g * 8;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
+  for (int s = 0; s < kMfmaSteps; ++s) {
     const int64_t k = kb + s * 32;
     const bool ok = k < K;
 #pragma unroll
     for (int t = 0; t < T; ++t) f.w[t][s] = ok ? ld16_stream(wrow[t] + k) : make_uint4(0, 0, 0, 0);
+#if EZ_MFMA_XP == 1
+    f.x[s] = make_uint4(unsigned(k), 1u, 2u, 3u);
+#else
     f.x[s] = (ok && mvalid) ? *reinterpret_cast<const uint4*>(xrow + k) : make_uint4(0, 0, 0, 0);
+#endif
   }
 }
 
 template <int T>
 __device__ __forceinline__ void mfma_step(f32x4_t (&acc)[T], const MfmaFrag<T>& f) {
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
+  for (int s = 0; s < kMfmaSteps; ++s) {
     const bf16x8_t bx = as_bf16x8(f.x[s]);
 #pragma unroll
     for (int t = 0; t < T; ++t)
@@ -210,8 +230,8 @@ __device__ __forceinline__ void mfma_step(f32x4_t (&acc)[T], const MfmaFrag<T>& 
 }
 
 template <int T, bool SILU>
-__global__ __launch_bounds__(kBlock) void linear_mfma_kernel(LinearArgs a) {
-  __shared__ float red[kWavesPerBlock][T][4][kWave];
+__global__ __launch_bounds__(kMfmaWaves * kWave) void linear_mfma_kernel(LinearArgs a) {
+  __shared__ float red[kMfmaWaves][T][4][kWave];
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const int i = lane & 15, g = lane >> 4;
   const int64_t m0 = int64_t(blockIdx.y) * 16;
@@ -229,12 +249,12 @@ __global__ __launch_bounds__(kBlock) void linear_mfma_kernel(LinearArgs a) {
   }
   const uint16_t* xrow = a.X + (mvalid ? m : 0) * a.ldx;
 
-  const int64_t nchunks = (a.K + 127) / 128;
+  const int64_t nchunks = (a.K + kMfmaChunk - 1) / kMfmaChunk;
 #if EZ_MFMA_INTERLEAVE
-  const int64_t cb = 0, ce = (nchunks - wave + kWavesPerBlock - 1) / kWavesPerBlock;  // local chunk count
-  auto chunk = [&](int64_t c) { return c * kWavesPerBlock + wave; };
+  const int64_t cb = 0, ce = (nchunks - wave + kMfmaWaves - 1) / kMfmaWaves;  // local chunk count
+  auto chunk = [&](int64_t c) { return c * kMfmaWaves + wave; };
 #else
-  const int64_t cb = nchunks * wave / kWavesPerBlock, ce = nchunks * (wave + 1) / kWavesPerBlock;
+  const int64_t cb = nchunks * wave / kMfmaWaves, ce = nchunks * (wave + 1) / kMfmaWaves;
   auto chunk = [&](int64_t c) { return c; };
 #endif
 
@@ -262,7 +282,8 @@ __global__ __launch_bounds__(kBlock) void linear_mfma_kernel(LinearArgs a) {
     for (int j = 0; j < 4; ++j) red[wave][t][j][lane] = acc[t][j];
   __syncthreads();
 
-  // Thread tid finalises output (j, l) = (tid / 64, tid % 64) of every tile.
+  // Thread tid < 256 finalises output (j, l) = (tid / 64, tid % 64) of every tile.
+  if (threadIdx.x >= 4 * kWave) return;
   const int j = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int64_t mo = m0 + (l & 15);
   if (mo >= a.M) return;
@@ -271,7 +292,7 @@ __global__ __launch_bounds__(kBlock) void linear_mfma_kernel(LinearArgs a) {
   for (int t = 0; t < T; ++t) {
     float sacc = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWavesPerBlock; ++w) sacc += red[w][t][j][l];
+    for (int w = 0; w < kMfmaWaves; ++w) sacc += red[w][t][j][l];
     v[t] = sacc;
   }
   const int rofs = 4 * (l >> 4) + j;
@@ -603,7 +624,7 @@ void launch_valu_m(const LinearArgs& a, hipStream_t s) {
 
 template <bool SILU>
 void launch_mfma(const LinearArgs& a, hipStream_t s) {
-  constexpr int T = SILU ? 2 : 1;
+  constexpr int T = SILU ? 2 : EZ_MFMA_T1;
   const int64_t blocks = SILU ? (a.N + 15) / 16 : (a.N + 16 * T - 1) / (16 * T);
   dim3 grid(unsigned(blocks), unsigned((a.M + 15) / 16));
   if (EZ_MFMA_LDS) {
@@ -611,7 +632,7 @@ void launch_mfma(const LinearArgs& a, hipStream_t s) {
     dim3 lgrid(unsigned(lblocks), unsigned((a.M + 15) / 16));
     hipLaunchKernelGGL((linear_mfma_lds_kernel<T>), lgrid, dim3(kBlock), 0, s, a);
   } else {
-    hipLaunchKernelGGL((linear_mfma_kernel<T, SILU>), grid, dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL((linear_mfma_kernel<T, SILU>), grid, dim3(kMfmaWaves * kWave), 0, s, a);
   }
 }
 

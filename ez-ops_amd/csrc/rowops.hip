@@ -407,6 +407,67 @@ extern "C" int ezops_reduce_sum_f32(const float* A, float* Out, int64_t n, void*
   return launch_status("reduce_sum_f32");
 }
 
+// MFMA peak probe: every wave keeps 8 independent 16x16x32 accumulator chains
+// busy for `iters` rounds (operands built from the lane id, so nothing folds).
+// One launch performs blocks * 4 waves * iters * 8 * 16384 flops.
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+template <int F16>
+__global__ __launch_bounds__(256) void probe_mfma_kernel(float* __restrict__ out, int64_t iters) {
+  const float lf = float(threadIdx.x & 63) * (1.0f / 64.0f);
+  if constexpr (F16 == 2) {  // bf16 32x32x16: 4 chains of 16-float accumulators, same flops per round
+    f32x16_t acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
+    bf16x8_t a, b;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { a[e] = __bf16(lf + e); b[e] = __bf16(1.0f - lf * e); }
+    for (int64_t i = 0; i < iters; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[j], 0, 0, 0);
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sum += acc[j][e];
+    if (sum == 1234.5f) out[0] = sum;
+    return;
+  }
+  f32x4_t acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  if constexpr (F16 == 1) {
+    f16x8_t a, b;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { a[e] = _Float16(lf + e); b[e] = _Float16(1.0f - lf * e); }
+    for (int64_t i = 0; i < iters; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[j], 0, 0, 0);
+  } else {
+    bf16x8_t a, b;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { a[e] = __bf16(lf + e); b[e] = __bf16(1.0f - lf * e); }
+    for (int64_t i = 0; i < iters; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[j], 0, 0, 0);
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) sum += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
+  if (sum == 1234.5f) out[0] = sum;  // keeps the chains alive; practically never stores
+}
+
+extern "C" int ezops_mfma_probe(int kind, float* out, int64_t blocks, int64_t iters, hipStream_t s) {
+  EZ_REQUIRE(kind >= 0 && kind <= 2, "mfma_probe: kind must be 0 (bf16), 1 (fp16) or 2 (bf16 32x32x16)");
+  EZ_REQUIRE(out && blocks >= 1 && blocks < (int64_t(1) << 31) && iters >= 1, "mfma_probe: bad arguments");
+  if (kind == 0) hipLaunchKernelGGL(probe_mfma_kernel<0>, dim3(unsigned(blocks)), dim3(256), 0, s, out, iters);
+  else if (kind == 1) hipLaunchKernelGGL(probe_mfma_kernel<1>, dim3(unsigned(blocks)), dim3(256), 0, s, out, iters);
+  else hipLaunchKernelGGL(probe_mfma_kernel<2>, dim3(unsigned(blocks)), dim3(256), 0, s, out, iters);
+  return launch_status("mfma_probe");
+}
+
 extern "C" int ezops_hbm_probe(int kind, float* a, const float* b, const float* c, int64_t n, float sc,
                                hipStream_t s) {
   EZ_REQUIRE(kind >= 0 && kind <= 4, "hbm_probe: kind must be 0..4");

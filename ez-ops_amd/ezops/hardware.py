@@ -1,0 +1,196 @@
+"""MI355X hardware profile for roofline analysis.
+
+Mirrors the reference's hardware-profile tooling:
+* ``SPECS`` / ``detect_profile`` / ``get_specs`` — the spec database
+  (benchmarks/hardware/gpu_specs.py), here with the one chip this backend runs on;
+* ``measure_hbm`` / ``measure_mfma`` — the calibration microbenchmarks
+  (benchmarks/hardware/memory/hbm_bandwidth.py, benchmarks/hardware/compute/matmul_peak.py),
+  here the library's own STREAM probe (``ezops_hbm_probe``) and MFMA chain probe
+  (``ezops_mfma_probe``) instead of CUDA kernels / torch matmuls;
+* ``generate_yaml`` / ``main`` — the profile writer (scripts/roofline_profile.py:72-241),
+  same YAML layout (theoretical + calibration; effective = theoretical * calibration);
+* ``load_profile`` — the loader the reference benches use (benchmarks/bench_gemv.py ``_load_profile``).
+
+Run ``python -m ezops.hardware`` on an MI355X to (re)write ``ezops/assets/mi355x.yaml``.
+"""
+
+from __future__ import annotations
+
+import argparse
+import math
+from pathlib import Path
+
+ASSETS = Path(__file__).resolve().parent / "assets"
+
+# Published dense peaks (no sparsity), FMA counted as 2 flops.
+SPECS = {
+    "mi355x": {
+        "names": ["AMD Instinct MI355X", "AMD Instinct MI350X"],
+        "arch": "gfx950",
+        "cu_count": 256,
+        "l2_cache_size": 4 * 1024 * 1024,      # per XCD (8 XCDs)
+        "mall_size": 256 * 1024 * 1024,        # Infinity Cache
+        "lds_per_cu": 160 * 1024,
+        "hbm_bw_gb": 8000.0,
+        "tensor_core_tflops": {"bf16": 2500.0, "fp16": 2500.0, "fp8": 5000.0, "fp32": 157.3},
+    },
+}
+
+_MFMA_KINDS = {"bf16": 0, "fp16": 1, "bf16_32x32": 2}
+_MFMA_FLOPS_PER_INSTR = 2 * 16 * 16 * 32
+
+
+def detect_profile(name: str = "", arch: str = "") -> str | None:
+    """Profile key for a device name / gcnArchName, or None."""
+    for key, spec in SPECS.items():
+        if spec["arch"] and arch and arch.split(":")[0] == spec["arch"]:
+            return key
+        if any(n.lower() in name.lower() for n in spec["names"]):
+            return key
+    return None
+
+
+def get_specs(profile: str) -> dict:
+    return SPECS[profile]
+
+
+def measure_hbm(n_bytes_per_array: int = 2 << 30, reps: int = 10) -> dict:
+    """STREAM triad (a = b + s*c) and streaming read over arrays >> MALL: best GB/s."""
+    import torch
+
+    from . import _hip
+
+    n = n_bytes_per_array // 4
+    a = torch.empty(n, dtype=torch.float32, device="cuda")
+    b = torch.rand(n, device="cuda")
+    c = torch.rand(n, device="cuda")
+    s = _hip.stream()
+    out = {}
+    for kind, name, nbytes in ((3, "triad", 12 * n), (4, "read", 4 * n)):
+        best = math.inf
+        for _ in range(reps + 2):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            _hip.call("ezops_hbm_probe", kind, a.data_ptr(), b.data_ptr(), c.data_ptr(), n, 1.5, s)
+            e1.record()
+            torch.cuda.synchronize()
+            best = min(best, e0.elapsed_time(e1))
+        out[name] = nbytes / (best * 1e-3) / 1e9
+    del a, b, c
+    torch.cuda.empty_cache()
+    return out
+
+
+def measure_mfma(dtype: str = "bf16", iters: int = 4096, reps: int = 10) -> float:
+    """Dense MFMA throughput (TFLOP/s) of independent v_mfma_f32_16x16x32 chains on every SIMD."""
+    import torch
+
+    from . import _hip
+
+    blocks = torch.cuda.get_device_properties(0).multi_processor_count * 8
+    sink = torch.zeros(4, device="cuda")
+    s = _hip.stream()
+    flops = blocks * 4 * iters * 8 * _MFMA_FLOPS_PER_INSTR
+    best = math.inf
+    for _ in range(reps + 2):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        _hip.call("ezops_mfma_probe", _MFMA_KINDS[dtype], sink.data_ptr(), blocks, iters, s)
+        e1.record()
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1))
+    return flops / (best * 1e-3) / 1e12
+
+
+def _fmt(coeff: float, unit_exp: int) -> str:
+    """`coeff` x 10^unit_exp in the reference's notation ('8000e9'); YAML reads it as text,
+    load_profile() converts."""
+    return f"{coeff:.1f}e{unit_exp}" if coeff != int(coeff) else f"{int(coeff)}e{unit_exp}"
+
+
+def generate_yaml(profile: str, gpu_name: str, hbm: dict, mfma_tflops: dict) -> str:
+    """Profile YAML in the reference's layout (assets/rtx_5060_ti.yaml)."""
+    spec = SPECS[profile]
+    lines = [
+        f"# GPU Profile: {gpu_name}",
+        "# Calibration: ezops_hbm_probe (STREAM triad, 3 x 2 GiB) and ezops_mfma_probe",
+        "# Written by: cd ez-ops_amd && python -m ezops.hardware",
+        "#",
+        "# Only store theoretical + calibration here.",
+        "# effective = theoretical * calibration is computed by load_profile().",
+        "",
+        f"gpu: {gpu_name}",
+        f"compute_capability: {spec['arch']}",
+        "",
+        f"sm_count: {spec['cu_count']}            # compute units",
+        f"l2_cache_size: {spec['l2_cache_size']}       # {spec['l2_cache_size'] >> 20} MB per XCD",
+        f"mall_size: {spec['mall_size']}       # {spec['mall_size'] >> 20} MB Infinity Cache",
+        f"shared_memory_per_sm: {spec['lds_per_cu']}       # {spec['lds_per_cu'] >> 10} KB LDS",
+        "",
+        "hbm:",
+        f"  theoretical: {_fmt(spec['hbm_bw_gb'], 9)}        # bytes/s, spec sheet",
+        f"  calibration: {hbm['triad'] / spec['hbm_bw_gb']:.3f}         # STREAM Triad",
+    ]
+    if "read" in hbm:
+        lines.append(f"  read_calibration: {hbm['read'] / spec['hbm_bw_gb']:.3f}    # streaming read (non-temporal)")
+    lines += ["", "tensor_core:"]
+    for dtype, theo in spec["tensor_core_tflops"].items():
+        lines.append(f"  {dtype}:")
+        lines.append(f"    theoretical: {_fmt(theo, 12)}     # FLOPS, spec sheet (dense)")
+        if dtype in mfma_tflops:
+            lines.append(f"    calibration: {mfma_tflops[dtype] / theo:.2f}")
+        lines.append("")
+    return "\n".join(lines)
+
+
+def load_profile(name_or_path: str | Path = "mi355x") -> dict:
+    """Parse a profile YAML and add effective peaks (theoretical * calibration)."""
+    import yaml
+
+    path = Path(name_or_path)
+    if not path.suffix:
+        path = ASSETS / f"{name_or_path}.yaml"
+    prof = yaml.safe_load(path.read_text())
+    hbm = prof["hbm"]
+    hbm["effective"] = float(hbm["theoretical"]) * float(hbm.get("calibration", 1.0))
+    if "read_calibration" in hbm:
+        hbm["read_effective"] = float(hbm["theoretical"]) * float(hbm["read_calibration"])
+    for entry in prof.get("tensor_core", {}).values():
+        entry["effective"] = float(entry["theoretical"]) * float(entry.get("calibration", 1.0))
+    return prof
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description="Generate the MI355X roofline profile YAML")
+    ap.add_argument("--output-dir", default=str(ASSETS))
+    ap.add_argument("--dtypes", default="bf16")
+    args = ap.parse_args(argv)
+
+    import torch
+
+    props = torch.cuda.get_device_properties(0)
+    profile = detect_profile(props.name, getattr(props, "gcnArchName", ""))
+    if profile is None:
+        print(f"unknown device {props.name!r}: only the MI355X profile is defined")
+        return 2
+    hbm = measure_hbm()
+    print(f"HBM triad {hbm['triad']:.0f} GB/s, streaming read {hbm['read']:.0f} GB/s")
+    mfma = {}
+    for dtype in [d.strip() for d in args.dtypes.split(",") if d.strip()]:
+        mfma[dtype] = measure_mfma(dtype)
+        print(f"MFMA {dtype} 16x16x32: {mfma[dtype]:.0f} TFLOP/s")
+        if dtype == "bf16":  # the larger tile shape can issue denser; keep the faster
+            big = measure_mfma("bf16_32x32")
+            print(f"MFMA bf16 32x32x16: {big:.0f} TFLOP/s")
+            mfma[dtype] = max(mfma[dtype], big)
+    text = generate_yaml(profile, SPECS[profile]["names"][0], hbm, mfma)
+    out = Path(args.output_dir) / f"{profile}.yaml"
+    out.parent.mkdir(parents=True, exist_ok=True)
+    out.write_text(text + "\n")
+    print(f"saved {out}")
+    print(text)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -178,6 +178,13 @@ int ezops_qwen3_dense_decode_bf16(const ezops_qwen3_layer* p, void* workspace,
 int ezops_hbm_probe(int kind, float* a, const float* b, const float* c, int64_t n, float s,
                     hipStream_t stream);
 
+/* MFMA peak probe for the hardware profile (replaces the torch-matmul sweep of
+ * benchmarks/hardware/compute/matmul_peak.py, used by
+ * scripts/roofline_profile.py:171-199): kind 0 = bf16, 1 = fp16
+ * v_mfma_f32_16x16x32 chains, 2 = bf16 v_mfma_f32_32x32x16 chains; every kind
+ * performs blocks * 4 * iters * 8 * 16384 flops per launch. */
+int ezops_mfma_probe(int kind, float* out, int64_t blocks, int64_t iters, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
