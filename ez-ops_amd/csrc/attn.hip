@@ -1,15 +1,418 @@
-// Standalone split-KV GQA decode attention kernel and its launcher.  The
-// per-block routine (and its design notes) is in attn_impl.h.
-#include "attn_impl.h"
+// Split-KV GQA decode attention for gfx950, with an optional fused Qwen3
+// prologue (q/k RMSNorm + RoPE + KV-cache write of the decoded token).
+//
+// Work unit = (sequence b, kv head).  A block of W waves serves one unit
+// split; its G = H / Hkv query heads share every K/V byte it loads, so K/V
+// cross HBM once per GQA group.  The 32-position tiles of a sequence are
+// dealt round-robin: wave w of split s takes tiles s*W + w,
+// s*W + w + nsplit*W, ...  The split count is planned on the host's bound
+// Lh of the live lengths (the capacity S when no bound is given); the
+// lengths themselves are read on the device.
+//
+// Per wave and tile:
+//   * scores S[h, p] = q_h . k_p on MFMA (v_mfma_f32_16x16x32_bf16): A = the
+//     G query rows (zero-padded to 16), B = 16 positions of K per sub-tile;
+//     a lane loads 16-byte pieces of K rows straight into the B operand
+//     (k-slot (lg, e) of step s = head dim 32 s + 8 lg + e, Q uses the same
+//     map), so one load instruction reads 64 contiguous bytes of 16 rows.
+//   * online softmax in the exp2 domain (scale * log2 e folded into S), the
+//     running max wave-uniform, row maxima by DPP.
+//   * O += P . V on VALU: V rows are read with fully coalesced 16-byte loads
+//     (one wave instruction covers 1 KiB of consecutive rows); P goes through
+//     a small LDS slice per wave and is read back as broadcasts.
+//   * every tile load is unconditional (rows past the live length read a
+//     clamp row): the next tile's K is requested right after the MFMAs and
+//     its V right after P.V, and each wait covers only the data it needs.
+// The first tile is requested before the length arrives (its addresses only
+// need Lh), behind a single scalar load of the length.  The W waves merge
+// (max, sum, O) through LDS; with more than one split the blocks write fp32
+// partials that attn_combine_kernel merges (the kernel boundary orders the
+// hand-off; an in-kernel arrival counter measured no faster on MI355X).
+#include "common.h"
+#include "internal.h"
 #include "status.h"
 #include "../../include/ezops_hip.h"
+
+#ifndef EZ_ATTN_TRACE
+#define EZ_ATTN_TRACE 0  // timing experiments only: per-wave phase timestamps
+#endif
 
 namespace ez {
 namespace {
 
-using attn::AttnWs;
-using attn::kMaxSplits;
-using attn::kTile;
+constexpr int kTile = 32;       // positions per wave iteration
+constexpr int kMaxSplits = 32;  // split partials the combine holds per lane
+constexpr float kLog2e = 1.4426950408889634f;
+
+#if EZ_ATTN_TRACE
+__device__ long long ez_attn_trace[65536 * 8];  // [block][wave][8] s_memrealtime stamps
+#define EZ_TRACE(k)                                                                                      \
+  do {                                                                                                   \
+    if (lane == 0) ez_attn_trace[(blockIdx.x * W + wave) * 8 + (k)] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#else
+#define EZ_TRACE(k) \
+  do {              \
+  } while (0)
+#endif
+
+// K tile rows t0 + 16u + li (clamped to `last`) into the MFMA B operand.
+template <int D, int NSUB>
+__device__ __forceinline__ void load_k_tile(const uint16_t* Kb, int64_t t0, int64_t last, int li, int lg,
+                                            uint4 (&kf)[NSUB][D / 32]) {
+#pragma unroll
+  for (int u = 0; u < NSUB; ++u) {
+    int64_t p = t0 + 16 * u + li;
+    p = p < last ? p : last;
+    const uint16_t* row = Kb + p * D + lg * 8;
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s) kf[u][s] = ld16_stream(row + 32 * s);
+  }
+}
+
+// V rows in row layout: lane (dc, rs) reads rows rs, rs + RPI, ... of the
+// tile (clamped to `last`), 16 B at column 8*dc.
+template <int D, int NPV>
+__device__ __forceinline__ void load_v_tile(const uint16_t* Vb, int64_t t0, int64_t last, int dc, int rs,
+                                            uint4 (&vf)[NPV]) {
+  constexpr int RPI = kWave / (D / 8);
+#pragma unroll
+  for (int j = 0; j < NPV; ++j) {
+    int64_t p = t0 + rs + RPI * j;
+    p = p < last ? p : last;
+    vf[j] = ld16_stream(Vb + p * D + dc * 8);
+  }
+}
+
+// Qwen3 per-head RMSNorm (fp32 statistics, weight) + half-split RoPE of one
+// bf16 head at `src`, rounded once to bf16 into `dst`.  One wave; lane l owns
+// the pairs (i, i + D/2), i = l, l + 64, ...  Operation order follows the
+// reference (ezops/ops/fused_qk_norm_rope.py:138-147).
+template <int D>
+__device__ __forceinline__ void norm_rope_head(const uint16_t* src, const uint16_t* w, const uint16_t* crow,
+                                               const uint16_t* srow, float eps, uint16_t* dst, int lane) {
+  constexpr int HALF = D / 2;
+  constexpr int NP = (HALF + kWave - 1) / kWave;
+  float x1[NP], x2[NP];
+  float ss = 0.f;
+#pragma unroll
+  for (int t = 0; t < NP; ++t) {
+    const int i = lane + t * kWave;
+    x1[t] = i < HALF ? bf2f(src[i]) : 0.f;
+    x2[t] = i < HALF ? bf2f(src[i + HALF]) : 0.f;
+    ss += x1[t] * x1[t] + x2[t] * x2[t];
+  }
+  const float r = rsqrtf(wave_reduce_uniform<false>(ss) / float(D) + eps);
+#pragma unroll
+  for (int t = 0; t < NP; ++t) {
+    const int i = lane + t * kWave;
+    if (i >= HALF) break;
+    float y1 = __fmul_rn(x1[t], r), y2 = __fmul_rn(x2[t], r);
+    if (w) {
+      y1 = __fmul_rn(y1, bf2f(w[i]));
+      y2 = __fmul_rn(y2, bf2f(w[i + HALF]));
+    }
+    float o1 = y1, o2 = y2;
+    if (crow) {
+      o1 = __fadd_rn(__fmul_rn(y1, bf2f(crow[i])), __fmul_rn(-y2, bf2f(srow[i])));
+      o2 = __fadd_rn(__fmul_rn(y2, bf2f(crow[i + HALF])), __fmul_rn(y1, bf2f(srow[i + HALF])));
+    }
+    dst[i] = f2bf(o1);
+    dst[i + HALF] = f2bf(o2);
+  }
+}
+
+// LAYER: q (and the decoded token's k, v) come from the bf16 QKV projection
+// row a.qkv + b*a.qkv_bs, columns [q | k | v]; q and k get the per-head
+// RMSNorm and RoPE at position kv_len - 1.  The unit's first block writes
+// the token's k, v into the cache slot; no block reads that slot: the token
+// enters the softmax as a virtual row from LDS (wave 0 of split 0).
+template <int D, int G, int W, bool LAYER>
+__global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int nsplit, float* opart, float* ml) {
+  constexpr int NS = D / 32;         // MFMA k-steps per 16-position sub-tile
+  constexpr int CPR = D / 8;         // 16-byte chunks per K/V row
+  constexpr int RPI = kWave / CPR;   // rows covered by one wave-wide V load
+  constexpr int NSUB = kTile / 16;   // MFMA sub-tiles per tile
+  constexpr int NPV = kTile / RPI;   // V rows per lane per tile
+  constexpr int GP = G <= 4 ? 4 : 8; // P row stride in LDS (float4 reads)
+  static_assert(G <= 8, "group size");
+
+  __shared__ __align__(16) float Ps[W][kTile][GP];
+  __shared__ __align__(16) float Os[W][G][D];
+  __shared__ float Ms[W][G], Ls[W][G];
+  __shared__ __align__(16) uint16_t Qs[LAYER ? G : 1][D];
+  __shared__ __align__(16) uint16_t Kn[LAYER ? D : 1], Vn[LAYER ? D : 1];
+
+  const int split = int(blockIdx.x % unsigned(nsplit)), unit = int(blockIdx.x / unsigned(nsplit));
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  EZ_TRACE(0);
+  const int li = lane & 15, lg = lane >> 4;
+  const int dc = lane % CPR, rs = lane / CPR;
+  const int kvh = unit % int(a.Hkv), b = unit / int(a.Hkv);
+  // The length is requested first, ahead of this wave's tile loads, and
+  // unconditionally (a dummy address without kv_lens), so that nothing waits
+  // for it before its first use.
+  const int32_t Lraw = *(a.kv_lens ? a.kv_lens + b : reinterpret_cast<const int32_t*>(a.K));
+  const uint16_t* Kb = a.K + (int64_t(b) * a.Hkv + kvh) * a.S * D;
+  const uint16_t* Vb = a.V + (int64_t(b) * a.Hkv + kvh) * a.S * D;
+  const int64_t h0 = int64_t(kvh) * G;  // first query head of the group
+  const float sl2 = a.scale * kLog2e;
+  const int64_t stride = int64_t(nsplit) * W * kTile;  // distance between a wave's tiles
+
+  int64_t t0 = (int64_t(split) * W + wave) * kTile;
+  uint4 kf[NSUB][NS], vf[NPV];
+  __builtin_amdgcn_sched_barrier(0);
+  load_k_tile<D, NSUB>(Kb, t0, a.Lh - 1, li, lg, kf);
+  load_v_tile<D, NPV>(Vb, t0, a.Lh - 1, dc, rs, vf);
+  __builtin_amdgcn_sched_barrier(0);
+
+  int64_t L = a.kv_lens ? int64_t(Lraw) : a.S;
+  L = L < 0 ? 0 : (L > a.Lh ? a.Lh : L);
+  EZ_TRACE(1);
+  // Cache rows read here: [0, Lc) (the layer's decoded token is the virtual row).
+  const int64_t Lc = LAYER ? (L > 0 ? L - 1 : 0) : L;
+  const int64_t cl = Lc > 0 ? Lc - 1 : 0;  // clamp row of later tiles
+
+  bf16x8_t qf[NS];
+  if constexpr (LAYER) {
+    const int64_t pos = L - 1;
+    const bool publisher = split == 0 && wave == W - 1;
+    if (L > 0) {
+      const uint16_t* row = a.qkv + int64_t(b) * a.qkv_bs;
+      const uint16_t* crow = a.cos ? a.cos + pos * D : nullptr;
+      const uint16_t* srow = a.sin ? a.sin + pos * D : nullptr;
+      for (int h = wave; h < G; h += W)
+        norm_rope_head<D>(row + (h0 + h) * D, a.qw, crow, srow, a.eps, &Qs[h][0], lane);
+      if (publisher) {
+        norm_rope_head<D>(row + a.H * D + int64_t(kvh) * D, a.kw, crow, srow, a.eps, Kn, lane);
+        const uint16_t* vrow = row + (a.H + a.Hkv) * D + int64_t(kvh) * D;
+        for (int i = lane; i < D; i += kWave) Vn[i] = vrow[i];
+      }
+    }
+    __syncthreads();  // Qs, Kn, Vn complete
+    if (publisher && L > 0) {
+      uint16_t* kdst = const_cast<uint16_t*>(Kb) + pos * D;
+      uint16_t* vdst = const_cast<uint16_t*>(Vb) + pos * D;
+      for (int i = lane; i < D; i += kWave) {
+        kdst[i] = Kn[i];
+        vdst[i] = Vn[i];
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (li < G) v = *reinterpret_cast<const uint4*>(&Qs[li][32 * s + lg * 8]);
+      qf[s] = as_bf16x8(v);
+    }
+  } else {
+    // Q operand: lane (li, lg) holds Q[h0 + li][s*32 + lg*8 .. +8] for step s.
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (li < G) v = *reinterpret_cast<const uint4*>(a.Q + ((b * a.H + h0 + li) * D) + 32 * s + lg * 8);
+      qf[s] = as_bf16x8(v);
+    }
+  }
+
+  float m_run[G], l_acc[G], o[G][8];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    m_run[h] = -INFINITY;
+    l_acc[h] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
+  }
+
+  EZ_TRACE(2);
+  for (int it = 0; t0 < Lc; t0 += stride, ++it) {
+    const int64_t tn = t0 + stride;
+    // ---- scores: acc[u][j] = S[head 4*lg + j][pos t0 + 16u + li]
+    f32x4_t acc[NSUB];
+#pragma unroll
+    for (int u = 0; u < NSUB; ++u) {
+      acc[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+        acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf[s], as_bf16x8(kf[u][s]), acc[u], 0, 0, 0);
+    }
+    if (EZ_ATTN_TRACE && it < 2) {
+      if (acc[0][0] == 1.2345e-30f) a.Out[0] = 1;  // the stamp follows the MFMA results
+      EZ_TRACE(3 + it);
+    }
+    load_k_tile<D, NSUB>(Kb, tn, cl, li, lg, kf);  // next K while this tile finishes
+
+    float mx[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      mx[j] = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < NSUB; ++u) {
+        const bool ok = t0 + 16 * u + li < Lc;
+        const float sv = ok ? acc[u][j] * sl2 : -INFINITY;
+        acc[u][j] = sv;
+        mx[j] = fmaxf(mx[j], sv);
+      }
+      mx[j] = dpp_row16<true>(mx[j]);
+    }
+    // ---- wave-uniform running max and rescale factors
+    float m_use[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float mt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx[h & 3]), 16 * (h >> 2)));
+      const float mn = fmaxf(m_run[h], mt);
+      const float alpha = (m_run[h] == -INFINITY) ? 0.f : exp2f(m_run[h] - mn);
+      m_run[h] = mn;
+      m_use[h] = (mn == -INFINITY) ? 0.f : mn;
+      l_acc[h] *= alpha;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[h][e] *= alpha;
+    }
+    // ---- P = exp2(S - m) into LDS as Ps[pos][head]
+    if (lg < GP / 4) {
+#pragma unroll
+      for (int u = 0; u < NSUB; ++u) {
+        float pv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int h = 4 * lg + j;
+          float mu = m_use[j < G ? j : 0];
+          if constexpr (G > 4) mu = (lg == 1) ? m_use[4 + j] : mu;
+          pv[j] = (h < G) ? exp2f(acc[u][j] - mu) : 0.f;
+        }
+        *reinterpret_cast<float4*>(&Ps[wave][16 * u + li][4 * lg]) = make_float4(pv[0], pv[1], pv[2], pv[3]);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // ---- O += P . V
+#pragma unroll
+    for (int j = 0; j < NPV; ++j) {
+      float pr[GP];
+#pragma unroll
+      for (int q4 = 0; q4 < GP / 4; ++q4) {
+        const float4 t = *reinterpret_cast<const float4*>(&Ps[wave][rs + RPI * j][4 * q4]);
+        pr[4 * q4 + 0] = t.x; pr[4 * q4 + 1] = t.y; pr[4 * q4 + 2] = t.z; pr[4 * q4 + 3] = t.w;
+      }
+      float v[8];
+      unpack8(vf[j], v);
+      if (t0 + rs + RPI * j >= Lc) {  // masked row: its cache bytes may be anything
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.f;
+      }
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        l_acc[h] += pr[h];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[h][e] = fmaf(pr[h], v[e], o[h][e]);
+      }
+    }
+    load_v_tile<D, NPV>(Vb, tn, cl, dc, rs, vf);  // next V
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  if constexpr (LAYER) {
+    // The decoded token as one more row of wave 0 of split 0: s_h = q_h . k
+    // (fp32 over the bf16 values the cache holds), then the same online
+    // update; P and V enter through the row-group-0 lanes only (the row
+    // groups are summed below).
+    if (split == 0 && wave == 0 && L > 0) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        float d = 0.f;
+        for (int i = lane; i < D; i += kWave) d = fmaf(bf2f(Qs[h][i]), bf2f(Kn[i]), d);
+        const float sv = wave_reduce_uniform<false>(d) * sl2;
+        const float mn = fmaxf(m_run[h], sv);
+        const float alpha = (m_run[h] == -INFINITY) ? 0.f : exp2f(m_run[h] - mn);
+        const float pv = rs == 0 ? exp2f(sv - mn) : 0.f;
+        m_run[h] = mn;
+        l_acc[h] = fmaf(l_acc[h], alpha, pv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[h][e] = fmaf(o[h][e], alpha, pv * bf2f(Vn[dc * 8 + e]));
+      }
+    }
+  }
+
+  EZ_TRACE(5);
+  // ---- merge the row groups of the wave (lanes with equal dc): VALU lane
+  // swaps, no LDS round trips
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    l_acc[h] = rowgroup_sum<CPR>(l_acc[h]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[h][e] = rowgroup_sum<CPR>(o[h][e]);
+  }
+  if (rs == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      *reinterpret_cast<float4*>(&Os[wave][h][dc * 8]) = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
+      *reinterpret_cast<float4*>(&Os[wave][h][dc * 8 + 4]) = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      Ms[wave][h] = m_run[h];
+      Ls[wave][h] = l_acc[h];
+    }
+  }
+  __syncthreads();
+
+  // ---- merge the W waves: thread handles (h, d) pairs
+  for (int idx = threadIdx.x; idx < G * D; idx += W * kWave) {
+    const int h = idx / D, d = idx % D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < W; ++w) M = fmaxf(M, Ms[w][h]);
+    float ov = 0.f, lv = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const float f = (Ms[w][h] == -INFINITY) ? 0.f : exp2f(Ms[w][h] - M);
+      ov = fmaf(f, Os[w][h][d], ov);
+      lv = fmaf(f, Ls[w][h], lv);
+    }
+    const int64_t hq = b * a.H + h0 + h;
+    if (nsplit == 1) {
+      a.Out[hq * D + d] = f2bf(lv > 0.f ? ov / lv : 0.f);
+    } else {
+      opart[(hq * nsplit + split) * D + d] = ov;
+      if (d == 0) *reinterpret_cast<float2*>(ml + (hq * nsplit + split) * 2) = make_float2(M, lv);
+    }
+  }
+  EZ_TRACE(6);
+}
+
+// Merge of one query head (b, h) with one thread per head dim: every thread
+// issues its nsplit partial loads at once (they do not depend on the
+// weights), while each wave turns the (max, sum) pairs (lane s = split s)
+// into normalised weights; one dependent memory round trip in total.
+//   out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s
+template <int D>
+__global__ __launch_bounds__(D) void attn_combine_kernel(AttnArgs a, int nsplit, const float* opart,
+                                                         const float* ml) {
+  static_assert(kMaxSplits <= kWave, "one split per lane");
+  const int64_t hq = blockIdx.x;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int d = threadIdx.x;
+  const float* op = opart + hq * nsplit * D + d;
+  float v[kMaxSplits];
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; ++s) v[s] = s < nsplit ? op[s * D] : 0.f;
+  const bool ok = lane < nsplit;
+  const float2 st = ok ? *reinterpret_cast<const float2*>(ml + hq * nsplit * 2 + 2 * lane)
+                       : make_float2(-INFINITY, 0.f);
+  const float M = wave_reduce_uniform<true>(st.x);
+  const float f = (st.x == -INFINITY) ? 0.f : exp2f(st.x - M);
+  const float tot = wave_reduce_uniform<false>(f * st.y);
+  const float wgt = tot > 0.f ? f / tot : 0.f;
+  float acc = 0.f;
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; ++s) {
+    const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), s));
+    acc = fmaf(w, v[s], acc);  // v[s] = 0 and w = 0 for s >= nsplit
+  }
+  a.Out[hq * D + d] = f2bf(acc);
+}
 
 int num_cus() {
   static int cus = 0;
@@ -24,13 +427,13 @@ int num_cus() {
 
 struct SplitPlan {
   int waves;
-  int64_t nsplit;
+  int nsplit;
 };
 
-// Splits per (b, kv head), planned on the cache capacity S: enough blocks to
-// keep every CU busy, at least one tile per wave at full capacity, and at
-// most kMaxSplits partials per merge.
-SplitPlan plan_splits(int64_t B, int64_t Hkv, int64_t S, int64_t G) {
+// Splits per (b, kv head), planned on the length bound Lh: enough blocks to
+// keep every CU busy, at least one tile per wave at length Lh, and at most
+// kMaxSplits partials per merge.
+SplitPlan plan_splits(int64_t B, int64_t Hkv, int64_t Lh, int64_t G) {
   const int64_t units = B * Hkv;
   const int64_t cus = num_cus();
   // 8-wave blocks for few units; group 8 keeps 4 waves (its accumulators need
@@ -38,105 +441,92 @@ SplitPlan plan_splits(int64_t B, int64_t Hkv, int64_t S, int64_t G) {
   const int waves = (units * 4 <= cus && G <= 4) ? 8 : 4;
   const int64_t target = waves == 8 ? 2 * cus : 8 * cus;  // blocks in flight
   int64_t ns = (target + units - 1) / units;
-  const int64_t max_ns = (S + int64_t(waves) * kTile - 1) / (int64_t(waves) * kTile);
+  const int64_t max_ns = (Lh + int64_t(waves) * kTile - 1) / (int64_t(waves) * kTile);
   if (ns > max_ns) ns = max_ns;
   if (ns > kMaxSplits) ns = kMaxSplits;
   if (ns < 1) ns = 1;
-  return {waves, ns};
+  return {waves, int(ns)};
 }
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
-#ifndef EZ_ATTN_MERGE_LAST
-#define EZ_ATTN_MERGE_LAST 0  // 1: the last block of a unit merges its splits (no combine launch)
-#endif
-constexpr bool kMergeLast = EZ_ATTN_MERGE_LAST;
-
-template <int D, int G, int W, int QSRC>
-__global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int64_t nsplit, AttnWs ws) {
-  attn::attn_block<D, G, W, QSRC, attn::kOutBf16, kMergeLast>(a, blockIdx.x % nsplit, blockIdx.x / nsplit, nsplit,
-                                                              ws);
-}
-
-// One wave per query head merges that head's split partials.
-template <int D>
-__global__ __launch_bounds__(kWave) void attn_combine_kernel(AttnArgs a, int64_t nsplit, AttnWs ws) {
-  attn::attn_combine<D, attn::kOutBf16>(a, blockIdx.x, nsplit, ws);
-}
-
-template <int D, int W, int LAYER>
-void launch_dw(const AttnArgs& a, const SplitPlan& pl, const AttnWs& ws, int64_t G, hipStream_t s) {
-  const dim3 grid{unsigned(a.B * a.Hkv * pl.nsplit), 1, 1}, block{unsigned(W * kWave), 1, 1};
-  switch (G) {
-    case 1: hipLaunchKernelGGL((attn_split_kernel<D, 1, W, LAYER>), grid, block, 0, s, a, pl.nsplit, ws); break;
-    case 2: hipLaunchKernelGGL((attn_split_kernel<D, 2, W, LAYER>), grid, block, 0, s, a, pl.nsplit, ws); break;
-    case 4: hipLaunchKernelGGL((attn_split_kernel<D, 4, W, LAYER>), grid, block, 0, s, a, pl.nsplit, ws); break;
-    default: break;  // group 8 launches from launch_d
-  }
-}
-
-template <int D, int LAYER>
-void launch_d(const AttnArgs& a, const SplitPlan& pl, const AttnWs& ws, int64_t G, hipStream_t s) {
-  const dim3 block{unsigned(pl.waves * kWave), 1, 1};
-  const dim3 grid{unsigned(a.B * a.Hkv * pl.nsplit), 1, 1};
+template <int D, bool LAYER>
+void launch_d(const AttnArgs& a, const SplitPlan& pl, float* opart, float* ml, int64_t G, hipStream_t s) {
+  const dim3 grid{unsigned(a.B * a.Hkv * pl.nsplit), 1, 1}, block{unsigned(pl.waves * kWave), 1, 1};
+#define EZ_LAUNCH(GG, WW) \
+  hipLaunchKernelGGL((attn_split_kernel<D, GG, WW, LAYER>), grid, block, 0, s, a, pl.nsplit, opart, ml)
   if (G == 8) {
-    hipLaunchKernelGGL((attn_split_kernel<D, 8, 4, LAYER>), grid, block, 0, s, a, pl.nsplit, ws);
+    EZ_LAUNCH(8, 4);
   } else if (pl.waves == 8) {
-    launch_dw<D, 8, LAYER>(a, pl, ws, G, s);
+    if (G == 1) EZ_LAUNCH(1, 8);
+    else if (G == 2) EZ_LAUNCH(2, 8);
+    else EZ_LAUNCH(4, 8);
   } else {
-    launch_dw<D, 4, LAYER>(a, pl, ws, G, s);
+    if (G == 1) EZ_LAUNCH(1, 4);
+    else if (G == 2) EZ_LAUNCH(2, 4);
+    else EZ_LAUNCH(4, 4);
   }
+#undef EZ_LAUNCH
 }
 
 }  // namespace
 
+// The workspace is planned on the capacity S, an upper bound for every Lh.
 size_t attn_workspace_size(int64_t B, int64_t H, int64_t Hkv, int64_t S, int64_t D) {
   if (B < 1 || H < 1 || Hkv < 1 || S < 1 || D < 1) return 0;
   const SplitPlan pl = plan_splits(B, Hkv, S, H / Hkv);
-  return align256(size_t(B * H * pl.nsplit * D) * 4) + align256(size_t(B * H * pl.nsplit * 2) * 4) +
-         align256(size_t(B * Hkv) * 4);
+  return align256(size_t(B * H * pl.nsplit * D) * 4) + align256(size_t(B * H * pl.nsplit * 2) * 4);
 }
 
 int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
   const bool layer = a.Q == nullptr;
   EZ_REQUIRE(a.K && a.V && a.Out && (!layer || a.qkv), "attn_decode: null pointer");
   EZ_REQUIRE(a.B >= 1 && a.H >= 1 && a.Hkv >= 1 && a.S >= 1, "attn_decode: bad shape");
+  EZ_REQUIRE(a.B * a.Hkv * kMaxSplits < (int64_t(1) << 31), "attn_decode: too many (batch, kv head) units");
   EZ_REQUIRE(a.H % a.Hkv == 0, "attn_decode: num_heads must be divisible by num_kv_heads");
   const int64_t G = a.H / a.Hkv;
   EZ_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "attn_decode: group size %lld not in {1,2,4,8}", (long long)G);
   EZ_REQUIRE(a.D == 64 || a.D == 128, "attn_decode: head_dim must be 64 or 128");
   EZ_REQUIRE((a.cos == nullptr) == (a.sin == nullptr), "attn_decode: cos and sin go together");
-  const SplitPlan pl = plan_splits(a.B, a.Hkv, a.S, G);
-  AttnWs w{};
-  if (pl.nsplit > 1) {
-    EZ_REQUIRE(ws && ws_bytes >= attn_workspace_size(a.B, a.H, a.Hkv, a.S, a.D),
-               "attn_decode: workspace too small (%zu < %zu)", ws_bytes,
-               attn_workspace_size(a.B, a.H, a.Hkv, a.S, a.D));
-    char* p = static_cast<char*>(ws);
-    w.opart = reinterpret_cast<float*>(p);
-    p += align256(size_t(a.B * a.H * pl.nsplit * a.D) * 4);
-    w.ml = reinterpret_cast<float*>(p);
-    p += align256(size_t(a.B * a.H * pl.nsplit * 2) * 4);
-    w.counters = reinterpret_cast<int*>(p);
-  }
+  EZ_REQUIRE(a.Lh >= 0, "attn_decode: max_kv_len must be >= 0");
   AttnArgs aa = a;
+  aa.Lh = (a.Lh == 0 || a.Lh > a.S || !a.kv_lens) ? a.S : a.Lh;
   if (aa.scale <= 0.f) aa.scale = 1.0f / sqrtf(float(a.D));
-  if (layer) {
-    if (a.D == 64) launch_d<64, attn::kQFromQkvBf16>(aa, pl, w, G, s);
-    else launch_d<128, attn::kQFromQkvBf16>(aa, pl, w, G, s);
-  } else {
-    if (a.D == 64) launch_d<64, attn::kQFromQ>(aa, pl, w, G, s);
-    else launch_d<128, attn::kQFromQ>(aa, pl, w, G, s);
+  const SplitPlan pl = plan_splits(aa.B, aa.Hkv, aa.Lh, G);
+  float *opart = nullptr, *ml = nullptr;
+  if (pl.nsplit > 1) {
+    const size_t need = attn_workspace_size(a.B, a.H, a.Hkv, a.S, a.D);
+    EZ_REQUIRE(ws && ws_bytes >= need, "attn_decode: workspace too small (%zu < %zu)", ws_bytes, need);
+    opart = static_cast<float*>(ws);
+    ml = reinterpret_cast<float*>(static_cast<char*>(ws) + align256(size_t(a.B * a.H * pl.nsplit * a.D) * 4));
   }
-  if (pl.nsplit > 1 && !kMergeLast) {
-    const dim3 grid{unsigned(a.B * a.H), 1, 1}, block{kWave, 1, 1};
-    if (a.D == 64) hipLaunchKernelGGL(attn_combine_kernel<64>, grid, block, 0, s, aa, pl.nsplit, w);
-    else hipLaunchKernelGGL(attn_combine_kernel<128>, grid, block, 0, s, aa, pl.nsplit, w);
+  if (layer) {
+    if (a.D == 64) launch_d<64, true>(aa, pl, opart, ml, G, s);
+    else launch_d<128, true>(aa, pl, opart, ml, G, s);
+  } else {
+    if (a.D == 64) launch_d<64, false>(aa, pl, opart, ml, G, s);
+    else launch_d<128, false>(aa, pl, opart, ml, G, s);
+  }
+  if (pl.nsplit > 1) {
+    const dim3 grid{unsigned(a.B * a.H), 1, 1}, block{unsigned(a.D), 1, 1};
+    if (a.D == 64) hipLaunchKernelGGL(attn_combine_kernel<64>, grid, block, 0, s, aa, pl.nsplit, opart, ml);
+    else hipLaunchKernelGGL(attn_combine_kernel<128>, grid, block, 0, s, aa, pl.nsplit, opart, ml);
   }
   return launch_status("attn_decode");
 }
 
 }  // namespace ez
+
+#if EZ_ATTN_TRACE
+extern "C" int ezops_attn_trace_read(void* host, size_t bytes) {
+  if (!host) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(ez::ez_attn_trace)) != hipSuccess) return -1;
+    return int(hipMemset(p, 0, bytes));
+  }
+  return int(hipMemcpyFromSymbol(host, HIP_SYMBOL(ez::ez_attn_trace), bytes, 0, hipMemcpyDeviceToHost));
+}
+#endif
 
 extern "C" size_t ezops_attn_decode_workspace_size(int64_t B, int64_t H, int64_t Hkv, int64_t S, int64_t D) {
   return ez::attn_workspace_size(B, H, Hkv, S, D);
@@ -144,7 +534,8 @@ extern "C" size_t ezops_attn_decode_workspace_size(int64_t B, int64_t H, int64_t
 
 extern "C" int ezops_attn_decode_bf16(const void* Q, const void* K, const void* V, void* Out, int64_t B,
                                       int64_t H, int64_t Hkv, int64_t S, int64_t D, const int32_t* kv_lens,
-                                      float scale, void* ws, size_t ws_bytes, hipStream_t stream) {
+                                      int64_t max_kv_len, float scale, void* ws, size_t ws_bytes,
+                                      hipStream_t stream) {
   EZ_REQUIRE(Q, "attn_decode: null pointer");
   ez::AttnArgs a{};
   a.Q = static_cast<const uint16_t*>(Q);
@@ -153,6 +544,7 @@ extern "C" int ezops_attn_decode_bf16(const void* Q, const void* K, const void* 
   a.Out = static_cast<uint16_t*>(Out);
   a.B = B; a.H = H; a.Hkv = Hkv; a.S = S; a.D = D;
   a.kv_lens = kv_lens;
+  a.Lh = max_kv_len;
   a.scale = scale;
   return ez::launch_attn(a, ws, ws_bytes, stream);
 }

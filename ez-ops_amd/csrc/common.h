@@ -104,6 +104,20 @@ __device__ __forceinline__ float dpp_row16(float v) {
   return v;
 }
 
+// Sum over the lanes that share lane % CPR (CPR = 8 or 16): DPP row_ror:8
+// pairs lanes l and l ^ 8 inside a 16-lane row, then the gfx950 lane swaps
+// v_permlane16_swap (rows 0<->1, 2<->3) and v_permlane32_swap (halves) add
+// the four rows.  Every lane ends with the bit-identical sum.
+template <int CPR>
+__device__ __forceinline__ float rowgroup_sum(float v) {
+  static_assert(CPR == 8 || CPR == 16, "row group width");
+  if constexpr (CPR == 8) v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, true));
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
 // Wave-uniform sum/max: DPP inside the four 16-lane rows, then the four row
 // results combined in a fixed order through readlane.
 template <bool MAX>

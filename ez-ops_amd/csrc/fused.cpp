@@ -11,8 +11,6 @@
 //                  out = o_proj + FFN(attn, hidden)
 #include <hip/hip_runtime.h>
 
-#include <cstdlib>
-#include <cstring>
 
 #include "internal.h"
 #include "status.h"
@@ -89,15 +87,6 @@ extern "C" int ezops_o_proj_ffn_bf16(const void* attn, const void* residual, con
 }
 
 namespace {
-// EZOPS_LAYER_PERSISTENT=1 selects the persistent single-launch layer
-// (layer.hip) where supported.  It is off by default: on MI355X its grid
-// barriers cost 8-13 us each (cross-XCD hand-offs through memory), more than
-// the ~1 us kernel boundaries of the multi-kernel graph it replaces.
-bool persistent_enabled() {
-  const char* e = std::getenv("EZOPS_LAYER_PERSISTENT");
-  return e && std::strcmp(e, "1") == 0;
-}
-
 size_t multi_kernel_ws(const ezops_qwen3_layer* p) {
   const int64_t QR = p->H * p->D, KVR = p->Hkv * p->D;
   return align256(size_t(p->B * p->HS) * 2)            // staged RMSNorm input (batch > 4)
@@ -109,9 +98,7 @@ size_t multi_kernel_ws(const ezops_qwen3_layer* p) {
 
 extern "C" size_t ezops_qwen3_layer_workspace_size(const ezops_qwen3_layer* p) {
   if (!p || p->B < 1 || p->H < 1 || p->Hkv < 1 || p->D < 1) return 0;
-  // Disjoint regions for the two paths (the persistent one is chosen per
-  // call), so neither path ever sees the other's data in its counters.
-  return align256(multi_kernel_ws(p)) + layer_persistent_ws(*p);
+  return multi_kernel_ws(p);
 }
 
 extern "C" int ezops_qwen3_dense_decode_bf16(const ezops_qwen3_layer* p, void* ws, size_t ws_bytes,
@@ -124,8 +111,6 @@ extern "C" int ezops_qwen3_dense_decode_bf16(const ezops_qwen3_layer* p, void* w
   EZ_REQUIRE(p->H % p->Hkv == 0, "qwen3_dense_decode: num_heads must be divisible by num_kv_heads");
   EZ_REQUIRE((p->cos == nullptr) == (p->sin == nullptr), "qwen3_dense_decode: cos and sin go together");
   EZ_REQUIRE(ws_bytes >= ezops_qwen3_layer_workspace_size(p), "qwen3_dense_decode: workspace too small");
-  if (persistent_enabled() && layer_persistent_supported(*p))
-    return launch_layer_persistent(*p, static_cast<char*>(ws) + align256(multi_kernel_ws(p)), s);
   const int64_t QR = p->H * p->D, KVR = p->Hkv * p->D, QKV = QR + 2 * KVR;
   Carve c{static_cast<char*>(ws)};
   uint16_t* xn = c.take<uint16_t>(size_t(p->B * p->HS) * 2);
@@ -151,6 +136,7 @@ extern "C" int ezops_qwen3_dense_decode_bf16(const ezops_qwen3_layer* p, void* w
   a.Out = att;
   a.B = p->B; a.H = p->H; a.Hkv = p->Hkv; a.S = p->S; a.D = p->D;
   a.kv_lens = p->kv_lens;
+  a.Lh = p->max_kv_len;
   a.scale = 0.f;
   a.qkv = qkv; a.qkv_bs = QKV;
   a.qw = static_cast<const uint16_t*>(p->q_norm_w);

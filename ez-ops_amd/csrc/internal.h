@@ -54,6 +54,7 @@ struct AttnArgs {
   uint16_t* Out;      // [B, H, D]
   int64_t B, H, Hkv, S, D;
   const int32_t* kv_lens;
+  int64_t Lh;         // bound on the live lengths for planning (0 = S); lengths above it are cut to it
   float scale;
   // Fused layer prologue (Q == NULL): q/k/v of the decoded token come from
   // the bf16 QKV projection (row b at qkv + b*qkv_bs, columns [q | k | v]);
@@ -64,18 +65,9 @@ struct AttnArgs {
   const uint16_t* qw; const uint16_t* kw;
   const uint16_t* cos; const uint16_t* sin;
   float eps;
-  // Persistent layer kernel only: fp32 QKV rows read with device-coherent
-  // loads, and an fp32 output written with device-coherent stores.
-  const float* qkv_f;
-  float* out_f;
 };
 size_t attn_workspace_size(int64_t B, int64_t H, int64_t Hkv, int64_t S, int64_t D);
 int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s);
 
-// Persistent single-launch layer kernel (layer.hip): batch <= 4, head_dim 128,
-// group 2 or 4, widths <= 12288, and one co-resident 512-thread block per CU.
-bool layer_persistent_supported(const ezops_qwen3_layer& L);
-size_t layer_persistent_ws(const ezops_qwen3_layer& L);
-int launch_layer_persistent(const ezops_qwen3_layer& L, void* ws, hipStream_t s);
 
 }  // namespace ez

@@ -16,7 +16,7 @@ import torch
 LIB_PATH = Path(os.environ.get("EZOPS_HIP_LIB", Path(__file__).resolve().parent / "_lib" / "libezops_hip.so"))
 
 EINVAL = -22
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _p, _i64, _f32, _sz, _i32 = C.c_void_p, C.c_int64, C.c_float, C.c_size_t, C.c_int
 
@@ -29,7 +29,7 @@ class Qwen3LayerParams(C.Structure):
         ("eps", _f32),
         ("hidden", _p), ("K_cache", _p), ("V_cache", _p), ("Wqkv", _p), ("Wo", _p), ("Wgu", _p), ("Wd", _p),
         ("in_norm_w", _p), ("q_norm_w", _p), ("k_norm_w", _p), ("post_norm_w", _p),
-        ("cos", _p), ("sin", _p), ("kv_lens", _p),
+        ("cos", _p), ("sin", _p), ("kv_lens", _p), ("max_kv_len", _i64),
         ("out", _p),
     ]
 
@@ -49,7 +49,7 @@ SIGNATURES: dict[str, tuple] = {
     "ezops_reduce_sum_workspace_size": (_sz, [_i64]),
     "ezops_reduce_sum_f32": (_i32, [_p, _p, _i64, _p, _sz, _p]),
     "ezops_attn_decode_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64]),
-    "ezops_attn_decode_bf16": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _f32, _p, _sz, _p]),
+    "ezops_attn_decode_bf16": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _f32, _p, _sz, _p]),
     "ezops_qk_norm_rope_bf16": (_i32, [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p,
                                        _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _f32, _p]),
     "ezops_o_proj_ffn_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),

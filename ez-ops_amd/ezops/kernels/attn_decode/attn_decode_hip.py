@@ -28,7 +28,14 @@ class AttnDecodeHipKernel(BaseKernel):
         self.B, self.H, self.S, self.D, self.Hkv = batch, num_heads, seq_len, head_dim, num_kv_heads
         self._ws = _hip.Workspace()
 
-    def __call__(self, Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, kv_lens: torch.Tensor | None = None):
+    def __call__(self, Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, kv_lens: torch.Tensor | None = None,
+                 max_kv_len: int = 0):
+        """``max_kv_len`` (extension, keyword): the caller's bound on the
+        ``kv_lens`` entries, 0 = seq_len.  It plans the split-KV grid and lets
+        the first K/V tiles be requested before the lengths are read; entries
+        above it are treated as ``max_kv_len``."""
+        if max_kv_len < 0:
+            raise ValueError(f"max_kv_len ({max_kv_len}) must be >= 0")
         dev = _hip.require_gpu(Q, K, V, kv_lens)
         bf = torch.bfloat16
         _hip.check(Q, "Q", (self.B, self.H, 1, self.D), bf)
@@ -40,6 +47,6 @@ class AttnDecodeHipKernel(BaseKernel):
         nbytes = _hip.size("ezops_attn_decode_workspace_size", self.B, self.H, self.Hkv, self.S, self.D)
         ws = self._ws.get(nbytes, dev)
         _hip.call("ezops_attn_decode_bf16", Q.data_ptr(), K.data_ptr(), V.data_ptr(), Out.data_ptr(),
-                  self.B, self.H, self.Hkv, self.S, self.D, _hip.ptr(kv_lens), 0.0, ws.data_ptr(), ws.numel(),
+                  self.B, self.H, self.Hkv, self.S, self.D, _hip.ptr(kv_lens), int(max_kv_len), 0.0, ws.data_ptr(), ws.numel(),
                   _hip.stream(dev))
         return Out

@@ -72,6 +72,7 @@ class Qwen3DenseDecodeHipKernel(BaseKernel):
             Wqkv=Wqkv.data_ptr(), Wo=Wo.data_ptr(), Wgu=Wgu.data_ptr(), Wd=Wd.data_ptr(),
             in_norm_w=_hip.ptr(nw[0]), q_norm_w=_hip.ptr(nw[1]), k_norm_w=_hip.ptr(nw[2]),
             post_norm_w=_hip.ptr(nw[3]), cos=_hip.ptr(cos), sin=_hip.ptr(sin), kv_lens=_hip.ptr(lens),
+            max_kv_len=max(self.kv_lens) if self.kv_lens else 0,
             out=out.data_ptr(),
         )
         pp = ctypes.byref(p)

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define EZOPS_HIP_ABI_VERSION 1
+#define EZOPS_HIP_ABI_VERSION 2
 #define EZOPS_EINVAL (-22)
 
 int ezops_hip_abi_version(void);
@@ -100,7 +100,10 @@ int ezops_reduce_sum_f32(const float* A, float* Out, int64_t n, void* workspace,
  * Q [B, H, D] (== [B, H, 1, D]), K/V [B, Hkv, S, D], Out [B, H, D]; bf16.
  * H % Hkv == 0, H / Hkv <= 16, D in {64, 128}.  kv_lens [B] int32 (NULL = S
  * for every sequence) limits sequence b to slots [0, kv_lens[b]).
- * scale <= 0 selects 1/sqrt(D).
+ * max_kv_len: the caller's bound on the kv_lens entries (0 = S), used to plan
+ * the split-KV grid and to request the first K/V tiles before the lengths
+ * are read; entries above it are treated as max_kv_len.  Ignored without
+ * kv_lens.  scale <= 0 selects 1/sqrt(D).
  * Replaces: flash_decode_tilelang_gqa_split (+ combine)
  * (ezops/kernels/attn_decode/attn_decode_tl.py:316-470, 617-627) and
  * attn_decode_cu (ezops/kernels/attn_decode/attn_decode_cu.cu:140-181)
@@ -108,8 +111,8 @@ int ezops_reduce_sum_f32(const float* A, float* Out, int64_t n, void* workspace,
 size_t ezops_attn_decode_workspace_size(int64_t B, int64_t H, int64_t Hkv, int64_t S, int64_t D);
 int ezops_attn_decode_bf16(const void* Q, const void* K, const void* V, void* Out, int64_t B,
                            int64_t H, int64_t Hkv, int64_t S, int64_t D, const int32_t* kv_lens,
-                           float scale, void* workspace, size_t workspace_bytes,
-                           hipStream_t stream);
+                           int64_t max_kv_len, float scale, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream);
 
 /* Qwen3 per-head QK RMSNorm + half-split RoPE + KV-cache write, one decode step.
  * q [B, H, D] (batch stride q_bstride elements), k/v [B, Hkv, D] (strides
@@ -162,6 +165,7 @@ typedef struct ezops_qwen3_layer {
   const void* cos;          /* [S, D] or NULL (no RoPE) */
   const void* sin;          /* [S, D] or NULL */
   const int32_t* kv_lens;   /* [B] int32 or NULL (= S for every sequence) */
+  int64_t max_kv_len;       /* bound on the kv_lens entries, 0 = S (see ezops_attn_decode_bf16) */
   /* output */
   void* out;                /* [B, HS] */
 } ezops_qwen3_layer;

@@ -31,8 +31,8 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_struct_layout_matches_header():
-    # int64 x7, float (+pad), then 15 pointers
-    assert ctypes.sizeof(_hip.Qwen3LayerParams) == 7 * 8 + 8 + 15 * 8
+    # int64 x7, float (+pad), then 16 eight-byte fields (15 pointers, max_kv_len)
+    assert ctypes.sizeof(_hip.Qwen3LayerParams) == 7 * 8 + 8 + 16 * 8
 
 
 def test_invalid_arguments_return_einval():

@@ -64,17 +64,6 @@ def test_fused_o_proj_ffn(batch, shape):
     np.testing.assert_allclose(n(out), n(ref), rtol=5e-2, atol=1e-1)
 
 
-@pytest.fixture(params=["multi_kernel", "persistent"])
-def layer_path(request, monkeypatch):
-    """The layer runs as a kernel chain by default; EZOPS_LAYER_PERSISTENT=1 selects
-    the persistent single-launch kernel for batch <= 4."""
-    if request.param == "persistent":
-        monkeypatch.setenv("EZOPS_LAYER_PERSISTENT", "1")
-    else:
-        monkeypatch.delenv("EZOPS_LAYER_PERSISTENT", raising=False)
-    return request.param
-
-
 def _layer(batch, seq_len, kwargs, **mode):
     torch.manual_seed(42)
     op = Qwen3DenseDecodeOp(batch, seq_len, backend="hip", **kwargs, **mode)
@@ -102,21 +91,20 @@ def _layer(batch, seq_len, kwargs, **mode):
 
 
 @pytest.mark.parametrize("batch,seq_len,num_kv_heads", [(1, 128, 8), (1, 1000, 8), (2, 1025, 8), (1, 4096, 4), (1, 1, 8)])
-def test_qwen3_dense_decode_reference_mode(batch, seq_len, num_kv_heads, layer_path):
+def test_qwen3_dense_decode_reference_mode(batch, seq_len, num_kv_heads):
     _layer(batch, seq_len, {**QWEN3_VL_2B, "num_kv_heads": num_kv_heads})
 
 
 @pytest.mark.parametrize("batch,seq_len", [(1, 16384), (3, 2048), (4, 4096), (16, 4096)])
-def test_qwen3_8b_layer_qwen3_mode(batch, seq_len, layer_path):
+def test_qwen3_8b_layer_qwen3_mode(batch, seq_len):
     rng = np.random.default_rng(4)
     lens = rng.integers(min(1024, seq_len), seq_len + 1, size=batch).tolist()
     _layer(batch, seq_len, {**QWEN3_8B, "num_kv_heads": 8}, kv_lens=lens, norm_weights=True, rope_theta=1e6)
 
 
-def test_qwen3_layer_persistent_repeated_calls(monkeypatch):
-    """The grid barrier and split counters return to zero after every call:
+def test_qwen3_layer_repeated_calls():
+    """Split partials and cache slots of one call never leak into the next:
     repeated calls with new hidden states stay correct."""
-    monkeypatch.setenv("EZOPS_LAYER_PERSISTENT", "1")
     torch.manual_seed(7)
     op = Qwen3DenseDecodeOp(1, 4096, backend="hip", kv_lens=[3000], norm_weights=True, rope_theta=1e6,
                             **QWEN3_8B, num_kv_heads=8)

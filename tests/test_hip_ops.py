@@ -135,6 +135,23 @@ def test_attn_decode(B, H, Hkv, S, D, ragged):
     assert torch.equal(out, out2)
 
 
+@pytest.mark.parametrize("B,S,bound", [(1, 16384, "max"), (3, 4096, "max"), (4, 8192, "cut"), (2, 3000, "over")])
+def test_attn_decode_max_kv_len(B, S, bound):
+    """max_kv_len plans the grid on the caller's length bound; lengths above
+    it are cut to it, a bound above the capacity means the capacity."""
+    torch.manual_seed(3)
+    op = AttnDecodeOp(B, 32, S, 128, backend="hip", num_kv_heads=8)
+    Q, K, V = op.gen_data()
+    lens = torch.randint(S // 8, S + 1, (B,), dtype=torch.int32)
+    hint = {"max": int(lens.max()), "cut": int(lens.float().mean()), "over": 2 * S}[bound]
+    out = op._kernel(Q, K, V, lens.to(DEV), max_kv_len=hint)
+    eff = np.minimum(lens.numpy().astype(np.int64), min(hint, S))
+    ref = oracle.attn_decode(n(Q)[:, :, 0], n(K), n(V), eff)
+    np.testing.assert_allclose(n(out)[:, :, 0], ref, **BF_TOL)
+    with pytest.raises(ValueError):
+        op._kernel(Q, K, V, lens.to(DEV), max_kv_len=-1)
+
+
 @pytest.mark.parametrize("B,S", [(1, 16384), (8, 4096)])
 def test_attn_decode_consecutive_calls_fresh_partials(B, S):
     """Split partials are handed between blocks through device-coherent
