@@ -26,9 +26,6 @@
 #ifndef EZ_GEMV_U
 #define EZ_GEMV_U 8         // 16-byte chunks per lane in flight per row (M <= 2)
 #endif
-#ifndef EZ_MFMA_INTERLEAVE
-#define EZ_MFMA_INTERLEAVE 0  // 1: wave w takes 128-wide K chunks w, w+4, ... (else a contiguous quarter)
-#endif
 
 namespace ez {
 namespace {
@@ -166,113 +163,205 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_valu_kernel(LinearArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// MFMA skinny GEMM for 16 batch rows (blockIdx.y selects the 16-row batch
-// block).  Block = 4 waves; the block owns T weight tiles of 16 rows and
-// wave w accumulates the w-th quarter of the K range (128-wide chunks).
+// MFMA skinny GEMM for M > 4 (blockIdx.y selects a 16-row batch block).  The
+// block owns one 16-row weight tile (T = 2: the gate and up tiles of the
+// same rows) and NW waves split the K range into contiguous 256-wide chunks.
 //
-// v_mfma_f32_16x16x32_bf16 operands, lane l = 16*g + i (g = l/16, i = l%16):
-//   A (weights):  A[i][g*8 .. g*8+7]   = W[row0 + i][k(g, s, 0..7)]
-//   B (batch):    B[g*8 .. g*8+7][i]   = X[m0 + i][k(g, s, 0..7)]
-//   C:            C[4*g + j][i], j = 0..3  -> weight row row0+4g+j, batch m0+i
-// The k-slot assignment k(g, s, e) = k0 + 32*s + 8*g + e (s = sub-step 0..3
-// of a 128-wide chunk) is the same for A and B, so the contraction is
-// exact, and each wave load instruction reads 64 contiguous bytes (4 lanes)
-// of each of its 16 weight rows.
-#ifndef EZ_MFMA_XP
-#define EZ_MFMA_XP 0  // timing experiments only
-#endif
-#ifndef EZ_MFMA_T1
-#define EZ_MFMA_T1 1  // 16-row weight tiles per wave (sharing each X fragment), plain epilogues
-#endif
-#ifndef EZ_MFMA_WAVES
-#define EZ_MFMA_WAVES 8   // waves per block of the MFMA kernel (the K range is split over them)
-#endif
-#ifndef EZ_MFMA_STEPS
-#define EZ_MFMA_STEPS 8   // 32-wide k-steps per fragment buffer (two buffers in flight)
-#endif
-constexpr int kMfmaWaves = EZ_MFMA_WAVES;
-constexpr int kMfmaSteps = EZ_MFMA_STEPS;
-constexpr int kMfmaChunk = 32 * kMfmaSteps;
+// v_mfma_f32_16x16x32_bf16 operands, lane l = 16 g + i:
+//   A (weights):  A[i][8g .. 8g+7]  = W[row0 + i][k0 + 32 s + 8 g + 0..7]
+//   B (batch):    B[8g .. 8g+7][i]  = X[m0 + i][k0 + 32 s + 8 g + 0..7]
+//   C:            C[4g + j][i]      -> weight row row0 + 4g + j, batch m0 + i
+// A register of the A operand spans 16 weight rows, so loading it straight
+// from HBM reads 64-byte pieces of 16 rows per instruction.  Instead the
+// load unit lands each chunk in LDS (global_load_lds_dwordx4) with 512-byte
+// row-contiguous reads, at 16-byte slot (r, c ^ r) for piece c of row r; the
+// A fragments are then ds_read_b128 with no bank conflicts (the 16 lanes of
+// a read hit 16 distinct slot columns).  Every wave owns a two-stage ring of
+// such tiles, so the loop has no block barrier.  X fragments (L2-resident
+// activations) are loaded straight into registers, one chunk ahead.
+constexpr int kMfmaKC = 256;                     // K elements per chunk
+constexpr int kMfmaSteps = kMfmaKC / 32;         // MFMA k-steps per chunk
+constexpr int kMfmaSlices = 16 * kMfmaKC / 512;  // 1 KiB DMA slices per 16-row tile and chunk
 
-template <int T>
-struct MfmaFrag {
-  uint4 w[T][kMfmaSteps];
-  uint4 x[kMfmaSteps];
-};
+__host__ __device__ constexpr int mfma_waves(int T) { return T == 1 ? 8 : 4; }
 
-template <int T, bool SILU>
-__device__ __forceinline__ void mfma_load(MfmaFrag<T>& f, const uint16_t* const (&wrow)[T], const uint16_t* xrow,
-                                          bool mvalid, int64_t c, int g, int64_t K) {
-  const int64_t kb = c * kMfmaChunk + g * 8;
-#pragma unroll
-  for (int s = 0; s < kMfmaSteps; ++s) {
-    const int64_t k = kb + s * 32;
-    const bool ok = k < K;
-#pragma unroll
-    for (int t = 0; t < T; ++t) f.w[t][s] = ok ? ld16_stream(wrow[t] + k) : make_uint4(0, 0, 0, 0);
-#if EZ_MFMA_XP == 1
-    f.x[s] = make_uint4(unsigned(k), 1u, 2u, 3u);
-#else
-    f.x[s] = (ok && mvalid) ? *reinterpret_cast<const uint4*>(xrow + k) : make_uint4(0, 0, 0, 0);
-#endif
-  }
+// s_waitcnt with vmcnt = N and the other counters unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int T>
-__device__ __forceinline__ void mfma_step(f32x4_t (&acc)[T], const MfmaFrag<T>& f) {
-#pragma unroll
-  for (int s = 0; s < kMfmaSteps; ++s) {
-    const bf16x8_t bx = as_bf16x8(f.x[s]);
-#pragma unroll
-    for (int t = 0; t < T; ++t)
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(f.w[t][s]), bx, acc[t], 0, 0, 0);
-  }
+typedef unsigned int u32x4v_t __attribute__((ext_vector_type(4)));
+
+// Reads the 8 A fragments of one chunk (one per k-step) from a DMA-landed
+// LDS tile and waits for them.  Written as one asm block without a memory
+// clobber: the compiler's own wait insertion treats any LDS read after an
+// LDS DMA as dependent on every outstanding load (vmcnt(0)), which would
+// drain the two-stage ring; the caller has already waited for exactly this
+// stage's DMA (wait_vm), and the volatile asm keeps its place relative to the
+// DMA that later refills the stage.
+__device__ __forceinline__ void lds_read_a8(const uint32_t (&addr)[kMfmaSteps], u32x4v_t (&r)[kMfmaSteps]) {
+  asm volatile(
+      "ds_read_b128 %0, %8\n\t"
+      "ds_read_b128 %1, %9\n\t"
+      "ds_read_b128 %2, %10\n\t"
+      "ds_read_b128 %3, %11\n\t"
+      "ds_read_b128 %4, %12\n\t"
+      "ds_read_b128 %5, %13\n\t"
+      "ds_read_b128 %6, %14\n\t"
+      "ds_read_b128 %7, %15\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+      : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]), "v"(addr[5]), "v"(addr[6]),
+        "v"(addr[7]));
+}
+static_assert(kMfmaSteps == 8, "lds_read_a8 reads 8 fragments");
+
+// Marks X fragment registers as redefined here, so no use of them (e.g. the
+// K-tail select) is scheduled right behind their loads, which would wait for
+// them there.
+__device__ __forceinline__ void xfrag_fence(u32x4v_t (&x)[kMfmaSteps]) {
+  asm volatile("" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]),
+                    "+v"(x[7]));
 }
 
-template <int T, bool SILU>
-__global__ __launch_bounds__(kMfmaWaves * kWave) void linear_mfma_kernel(LinearArgs a) {
-  __shared__ float red[kMfmaWaves][T][4][kWave];
+template <int T, bool SILU, int CPW>
+__global__ __launch_bounds__(mfma_waves(T) * kWave) void linear_mfma_kernel(LinearArgs a) {
+  constexpr int NW = mfma_waves(T);
+  constexpr int XN = kMfmaSteps;         // X loads per chunk
+  constexpr int DN = T * kMfmaSlices;    // DMA slices per chunk
+  // One array per ring stage: distinct LDS objects.
+  __shared__ __align__(16) uint4 Wl0[NW][T][kMfmaSlices][kWave];
+  __shared__ __align__(16) uint4 Wl1[NW][T][kMfmaSlices][kWave];
+  __shared__ float red[NW][T][4][kWave];
+
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const int i = lane & 15, g = lane >> 4;
   const int64_t m0 = int64_t(blockIdx.y) * 16;
   const int64_t m = m0 + i;
-  const bool mvalid = m < a.M;
+  const int64_t row0 = int64_t(blockIdx.x) * 16;
 
-  int64_t tile0[T];
-  const uint16_t* wrow[T];
+  // DMA lane roles: slice q of a chunk holds rows 2q, 2q+1 (lanes 0-31, 32-63);
+  // lane piece cs = lane & 31 stores the row's 16-byte piece cs ^ r.
+  const int dr = lane >> 5, cs = lane & 31;
+  const uint16_t* wrow[T][kMfmaSlices];
 #pragma unroll
-  for (int t = 0; t < T; ++t) {
-    tile0[t] = SILU ? int64_t(blockIdx.x) * 16 : (int64_t(blockIdx.x) * T + t) * 16;
-    int64_t row = tile0[t] + i;
-    if (row >= a.N) row = a.N - 1;
-    wrow[t] = ((SILU && t == 1) ? a.W2 : a.W) + row * a.K;
-  }
-  const uint16_t* xrow = a.X + (mvalid ? m : 0) * a.ldx;
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int q = 0; q < kMfmaSlices; ++q) {
+      int64_t row = row0 + 2 * q + dr;
+      if (row >= a.N) row = a.N - 1;
+      wrow[t][q] = ((SILU && t == 1) ? a.W2 : a.W) + row * a.K;
+    }
+  // Rows past M read row 0: their outputs are never stored.
+  const uint16_t* xrow = a.X + (m < a.M ? m : 0) * a.ldx;
 
-  const int64_t nchunks = (a.K + kMfmaChunk - 1) / kMfmaChunk;
-#if EZ_MFMA_INTERLEAVE
-  const int64_t cb = 0, ce = (nchunks - wave + kMfmaWaves - 1) / kMfmaWaves;  // local chunk count
-  auto chunk = [&](int64_t c) { return c * kMfmaWaves + wave; };
-#else
-  const int64_t cb = nchunks * wave / kMfmaWaves, ce = nchunks * (wave + 1) / kMfmaWaves;
-  auto chunk = [&](int64_t c) { return c; };
-#endif
+  const int64_t nchunks = (a.K + kMfmaKC - 1) / kMfmaKC;
+  const int64_t cb = nchunks * wave / NW, ce = nchunks * (wave + 1) / NW;
+
+  auto dma = [&](int64_t c, uint4 (*stage)[kMfmaSlices][kWave]) {
+    const int64_t k0 = c * kMfmaKC;
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int q = 0; q < kMfmaSlices; ++q) {
+        const int r = 2 * q + dr;
+        int64_t k = k0 + int64_t(cs ^ r) * 8;
+        k = k < a.K ? k : a.K - 8;  // past K: real weights, zeroed at use
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(wrow[t][q] + k),
+                                         (__attribute__((address_space(3))) void*)(&stage[t][q][0]), 16, 0, 0);
+      }
+  };
+  // Unconditional loads from clamped addresses: no branch around a pending load.
+  auto xload = [&](int64_t c, u32x4v_t (&x)[kMfmaSteps]) {
+#pragma unroll
+    for (int s = 0; s < kMfmaSteps; ++s) {
+      const int64_t k = c * kMfmaKC + 32 * s + 8 * g;
+      x[s] = *reinterpret_cast<const u32x4v_t*>(xrow + (k < a.K ? k : 0));
+    }
+  };
 
   f32x4_t acc[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // Two fragment buffers: chunk c lives in buffer (c - cb) % 2 and its buffer
-  // is refilled with chunk c + 2 right after its MFMAs are issued.
-  MfmaFrag<T> fa, fb;
-  if (cb < ce) mfma_load<T, SILU>(fa, wrow, xrow, mvalid, chunk(cb), g, a.K);
-  if (cb + 1 < ce) mfma_load<T, SILU>(fb, wrow, xrow, mvalid, chunk(cb + 1), g, a.K);
-  for (int64_t c = cb; c < ce; c += 2) {
-    mfma_step<T>(acc, fa);
-    if (c + 2 < ce) mfma_load<T, SILU>(fa, wrow, xrow, mvalid, chunk(c + 2), g, a.K);
-    if (c + 1 < ce) {
-      mfma_step<T>(acc, fb);
-      if (c + 3 < ce) mfma_load<T, SILU>(fb, wrow, xrow, mvalid, chunk(c + 3), g, a.K);
+  const bool ktail = a.K % kMfmaKC != 0;
+  auto compute = [&](int64_t c, const uint4 (*stage)[kMfmaSlices][kWave], u32x4v_t (&x)[kMfmaSteps]) {
+    xfrag_fence(x);
+    u32x4v_t af[T][kMfmaSteps];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      uint32_t addr[kMfmaSteps];
+#pragma unroll
+      for (int s = 0; s < kMfmaSteps; ++s)
+        addr[s] = uint32_t(reinterpret_cast<uintptr_t>(
+            (__attribute__((address_space(3))) const uint4*)(&stage[t][i >> 1][(i & 1) * 32 + ((4 * s + g) ^ i)])));
+      lds_read_a8(addr, af[t]);
+    }
+#pragma unroll
+    for (int s = 0; s < kMfmaSteps; ++s) {
+      u32x4v_t xv = x[s];
+      if (ktail && c * kMfmaKC + 32 * s + 8 * g >= a.K) {  // past K: both operands zero
+        xv = u32x4v_t{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int t = 0; t < T; ++t) af[t][s] = u32x4v_t{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, af[t][s]),
+                                                         __builtin_bit_cast(bf16x8_t, xv), acc[t], 0, 0, 0);
+    }
+  };
+
+  // Two-stage ring: chunk c lives in stage (c - cb) % 2 and X buffer xa/xb;
+  // after its MFMAs the stage is refilled with chunk c + 2.  Issue order per
+  // chunk is [DMA slices][X loads], so waiting for chunk c leaves exactly the
+  // next chunk's loads outstanding.  CPW > 0 (chunks per wave known at
+  // compile time: the model shapes) unrolls the ring completely.
+  u32x4v_t xa[kMfmaSteps], xb[kMfmaSteps];
+  if constexpr (CPW > 0) {
+    dma(cb, Wl0[wave]);
+    xload(cb, xa);
+    if constexpr (CPW > 1) {
+      dma(cb + 1, Wl1[wave]);
+      xload(cb + 1, xb);
+    }
+#pragma unroll
+    for (int cc = 0; cc < CPW; ++cc) {
+      if (cc + 1 < CPW) wait_vm<DN + XN>(); else wait_vm<0>();
+      auto& x = (cc & 1) ? xb : xa;
+      auto* stage = (cc & 1) ? Wl1[wave] : Wl0[wave];
+      compute(cb + cc, stage, x);
+      if (cc + 2 < CPW) {
+        dma(cb + cc + 2, stage);
+        xload(cb + cc + 2, x);
+      }
+    }
+  } else {
+    if (cb < ce) {
+      dma(cb, Wl0[wave]);
+      xload(cb, xa);
+    }
+    if (cb + 1 < ce) {
+      dma(cb + 1, Wl1[wave]);
+      xload(cb + 1, xb);
+    }
+    for (int64_t c = cb; c < ce; c += 2) {
+      if (c + 1 < ce) wait_vm<DN + XN>(); else wait_vm<0>();
+      compute(c, Wl0[wave], xa);
+      if (c + 2 < ce) {
+        dma(c + 2, Wl0[wave]);
+        xload(c + 2, xa);
+      }
+      if (c + 1 < ce) {
+        if (c + 2 < ce) wait_vm<DN + XN>(); else wait_vm<0>();
+        compute(c + 1, Wl1[wave], xb);
+        if (c + 3 < ce) {
+          dma(c + 3, Wl1[wave]);
+          xload(c + 3, xb);
+        }
+      }
     }
   }
 
@@ -282,7 +371,7 @@ __global__ __launch_bounds__(kMfmaWaves * kWave) void linear_mfma_kernel(LinearA
     for (int j = 0; j < 4; ++j) red[wave][t][j][lane] = acc[t][j];
   __syncthreads();
 
-  // Thread tid < 256 finalises output (j, l) = (tid / 64, tid % 64) of every tile.
+  // Thread tid < 256 finalises output (j, l) = (tid / 64, tid % 64).
   if (threadIdx.x >= 4 * kWave) return;
   const int j = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int64_t mo = m0 + (l & 15);
@@ -292,20 +381,11 @@ __global__ __launch_bounds__(kMfmaWaves * kWave) void linear_mfma_kernel(LinearA
   for (int t = 0; t < T; ++t) {
     float sacc = 0.f;
 #pragma unroll
-    for (int w = 0; w < kMfmaWaves; ++w) sacc += red[w][t][j][l];
+    for (int w = 0; w < NW; ++w) sacc += red[w][t][j][l];
     v[t] = sacc;
   }
-  const int rofs = 4 * (l >> 4) + j;
-  if (SILU) {
-    const int64_t n = tile0[0] + rofs;
-    if (n < a.N) store_out(a, mo, n, v[0], v[1]);
-  } else {
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-      const int64_t n = tile0[t] + rofs;
-      if (n < a.N) store_out(a, mo, n, v[t], 0.f);
-    }
-  }
+  const int64_t n = row0 + 4 * (l >> 4) + j;
+  if (n < a.N) store_out(a, mo, n, v[0], SILU ? v[1] : 0.f);
 }
 
 // ---------------------------------------------------------------------------
@@ -423,124 +503,6 @@ __global__ __launch_bounds__(kBlock) void gemv_rows_kernel(LinearArgs a) {
   }
 }
 
-// ---------------------------------------------------------------------------
-// LDS-staged MFMA skinny GEMM (M > 4).  The block owns T 16-row weight tiles
-// (T = 2: the gate and up tiles of the same rows) and streams K in 512-wide
-// chunks.  Weight rows are read with row-contiguous loads (a wave instruction
-// covers 4 rows x 256 B... in 16-byte pieces, 1 KiB of each row per chunk),
-// parked in registers while the previous chunk is multiplied, then written to
-// LDS, from where the MFMA fragments are read.  The 4 waves split each
-// chunk's 16 k-steps (wave w takes steps w, w+4, ...) and their partial tiles
-// are summed through LDS at the end.
-constexpr int kKC = 512;             // K elements per chunk
-constexpr int kRowPad = kKC + 8;     // LDS row stride in bf16 (16 B pad against bank conflicts)
-constexpr int kPieces = kKC / 8;     // 16-byte pieces per row per chunk
-
-template <int T>
-__global__ __launch_bounds__(kBlock) void linear_mfma_lds_kernel(LinearArgs a) {
-  constexpr bool SILU = T == 2;
-  constexpr int WROWS = 16 * T;
-  constexpr int WP = WROWS * kPieces / kBlock;  // weight pieces per thread per chunk
-  constexpr int XP = 16 * kPieces / kBlock;     // activation pieces per thread per chunk
-  __shared__ __align__(16) uint16_t Ws[WROWS][kRowPad];
-  __shared__ __align__(16) uint16_t Xs[16][kRowPad];
-  __shared__ float red[kWavesPerBlock][T][4][kWave];
-
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
-  const int i = lane & 15, g = lane >> 4;
-  const int64_t m0 = int64_t(blockIdx.y) * 16;
-  const int64_t n0 = int64_t(blockIdx.x) * (SILU ? 16 : WROWS);
-  const int64_t nchunks = (a.K + kKC - 1) / kKC;
-
-  // Row bases of the pieces this thread stages (piece p = u*kBlock + tid).
-  auto wsrc = [&](int u) -> const uint16_t* {
-    const int p = u * kBlock + tid, r = p / kPieces;
-    int64_t row = n0 + (SILU ? (r & 15) : r);
-    if (row >= a.N) row = a.N - 1;
-    return ((SILU && r >= 16) ? a.W2 : a.W) + row * a.K + (p % kPieces) * 8;
-  };
-  auto xsrc = [&](int u) -> const uint16_t* {
-    const int p = u * kBlock + tid, r = p / kPieces;
-    const int64_t m = m0 + r < a.M ? m0 + r : a.M - 1;
-    return a.X + m * a.ldx + (p % kPieces) * 8;
-  };
-
-  uint4 wr[WP], xr[XP];
-  auto fetch = [&](int64_t c) {
-    const int64_t k0 = c * kKC;
-#pragma unroll
-    for (int u = 0; u < WP; ++u) {
-      const int64_t k = k0 + ((u * kBlock + tid) % kPieces) * 8;
-      wr[u] = k < a.K ? ld16_stream(wsrc(u) + k0) : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int u = 0; u < XP; ++u) {
-      const int p = u * kBlock + tid;
-      const int64_t k = k0 + (p % kPieces) * 8;
-      xr[u] = (k < a.K && m0 + p / kPieces < a.M) ? *reinterpret_cast<const uint4*>(xsrc(u) + k0)
-                                                   : make_uint4(0, 0, 0, 0);
-    }
-  };
-  auto park = [&]() {
-#pragma unroll
-    for (int u = 0; u < WP; ++u) {
-      const int p = u * kBlock + tid;
-      *reinterpret_cast<uint4*>(&Ws[p / kPieces][(p % kPieces) * 8]) = wr[u];
-    }
-#pragma unroll
-    for (int u = 0; u < XP; ++u) {
-      const int p = u * kBlock + tid;
-      *reinterpret_cast<uint4*>(&Xs[p / kPieces][(p % kPieces) * 8]) = xr[u];
-    }
-  };
-
-  f32x4_t acc[T];
-#pragma unroll
-  for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  if (nchunks > 0) fetch(0);
-  for (int64_t c = 0; c < nchunks; ++c) {
-    __syncthreads();  // previous chunk's fragments have been read
-    park();
-    __syncthreads();
-    if (c + 1 < nchunks) fetch(c + 1);  // next chunk streams while this one is multiplied
-#pragma unroll
-    for (int s = wave; s < kKC / 32; s += kWavesPerBlock) {
-      const bf16x8_t bx = as_bf16x8(*reinterpret_cast<const uint4*>(&Xs[i][32 * s + 8 * g]));
-#pragma unroll
-      for (int t = 0; t < T; ++t)
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            as_bf16x8(*reinterpret_cast<const uint4*>(&Ws[16 * t + i][32 * s + 8 * g])), bx, acc[t], 0, 0, 0);
-    }
-  }
-
-#pragma unroll
-  for (int t = 0; t < T; ++t)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) red[wave][t][j][lane] = acc[t][j];
-  __syncthreads();
-
-  const int j = tid >> 6, l = tid & 63;
-  const int64_t mo = m0 + (l & 15);
-  if (mo >= a.M) return;
-  float v[T];
-#pragma unroll
-  for (int t = 0; t < T; ++t) {
-    float sacc = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWavesPerBlock; ++w) sacc += red[w][t][j][l];
-    v[t] = sacc;
-  }
-  const int64_t n = n0 + 4 * (l >> 4) + j;
-  if (SILU) {
-    if (n < a.N) store_out(a, mo, n, v[0], v[1]);
-  } else {
-#pragma unroll
-    for (int t = 0; t < T; ++t)
-      if (n + 16 * t < a.N) store_out(a, mo, n + 16 * t, v[t], 0.f);
-  }
-}
-
 // Scalar fallback for K % 8 != 0 or unaligned operands: one wave per output
 // row, plain bf16 loads.
 __global__ __launch_bounds__(kBlock) void linear_scalar_kernel(LinearArgs a) {
@@ -618,22 +580,22 @@ void launch_valu_m(const LinearArgs& a, hipStream_t s) {
   }
 }
 
-#ifndef EZ_MFMA_LDS
-#define EZ_MFMA_LDS 0  // 1: LDS-staged MFMA kernel for M > 4; 0: register-operand kernel
-#endif
-
 template <bool SILU>
 void launch_mfma(const LinearArgs& a, hipStream_t s) {
-  constexpr int T = SILU ? 2 : EZ_MFMA_T1;
-  const int64_t blocks = SILU ? (a.N + 15) / 16 : (a.N + 16 * T - 1) / (16 * T);
-  dim3 grid(unsigned(blocks), unsigned((a.M + 15) / 16));
-  if (EZ_MFMA_LDS) {
-    const int64_t lblocks = (a.N + 15) / 16;  // one (or one gate+up pair of) 16-row tile(s) per block
-    dim3 lgrid(unsigned(lblocks), unsigned((a.M + 15) / 16));
-    hipLaunchKernelGGL((linear_mfma_lds_kernel<T>), lgrid, dim3(kBlock), 0, s, a);
-  } else {
-    hipLaunchKernelGGL((linear_mfma_kernel<T, SILU>), grid, dim3(kMfmaWaves * kWave), 0, s, a);
+  constexpr int T = SILU ? 2 : 1;
+  constexpr int NW = mfma_waves(T);
+  const dim3 grid(unsigned((a.N + 15) / 16), unsigned((a.M + 15) / 16)), block(NW * kWave);
+  const int64_t nchunks = (a.K + kMfmaKC - 1) / kMfmaKC;
+  const int64_t cpw = nchunks % NW == 0 ? nchunks / NW : 0;
+#define EZ_MFMA_LAUNCH(C) hipLaunchKernelGGL((linear_mfma_kernel<T, SILU, C>), grid, block, 0, s, a)
+  switch (cpw) {
+    case 1: EZ_MFMA_LAUNCH(1); break;
+    case 2: EZ_MFMA_LAUNCH(2); break;
+    case 4: EZ_MFMA_LAUNCH(4); break;
+    case 6: EZ_MFMA_LAUNCH(6); break;
+    default: EZ_MFMA_LAUNCH(0); break;
   }
+#undef EZ_MFMA_LAUNCH
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -662,7 +624,8 @@ int launch_linear(const LinearArgs& a, hipStream_t s) {
   } else {
     // M > 4: the RMSNorm'd input is staged once as bf16(x * rsqrt(mean x^2 +
     // eps) * w) (the reference's staging) into the caller's workspace, then
-    // a plain MFMA GEMM runs on it.
+    // a plain MFMA GEMM runs on it.  (Normalising inside the GEMM repeats the
+    // work in every block of 16 weight rows: measured slower than staging.)
     LinearArgs b = a;
     if (a.norm) {
       EZ_REQUIRE(a.xn_ws, "linear: RMSNorm prologue with M > 4 needs a workspace of M*K bf16");

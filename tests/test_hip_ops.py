@@ -255,13 +255,14 @@ def test_golden_qk_norm_rope_through_abi(golden):
         np.testing.assert_array_equal(n(Kc)[b, :, p], n(ko)[b])
 
 
-@pytest.mark.parametrize("M", [1, 3, 8, 16])
+@pytest.mark.parametrize("M", [1, 3, 8, 16, 20])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3])
 @pytest.mark.parametrize("norm", [0, 1])
-def test_linear_stage_epilogues(M, epi, norm):
-    """ezops_linear_stage_bf16: RMSNorm prologue x epilogues, VALU (M <= 4) and MFMA (M > 4) paths."""
-    rng = np.random.default_rng(100 * M + 10 * epi + norm)
-    N, K = 192, 512
+@pytest.mark.parametrize("N,K", [(192, 512), (200, 1032)])
+def test_linear_stage_epilogues(M, epi, norm, N, K):
+    """ezops_linear_stage_bf16: RMSNorm prologue x epilogues, VALU (M <= 4) and MFMA (M > 4) paths,
+    with partial weight tiles, partial K chunks and partial batch blocks."""
+    rng = np.random.default_rng(100 * M + 10 * epi + norm + K)
     X = oracle.bf16(rng.standard_normal((M, K)).astype(np.float32))
     W = oracle.bf16(rng.standard_normal((N, K)).astype(np.float32) * K ** -0.5)
     W2 = oracle.bf16(rng.standard_normal((N, K)).astype(np.float32) * K ** -0.5)
