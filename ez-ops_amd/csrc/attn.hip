@@ -122,6 +122,14 @@ __device__ __forceinline__ void norm_rope_head(const uint16_t* src, const uint16
   }
 }
 
+// Output element (query head hq = b*H + h, dim d): row-major [B, H*D], or the
+// MFMA-packed layout of that matrix when it feeds the layer's batched o_proj.
+__device__ __forceinline__ int64_t out_index(const AttnArgs& a, int64_t hq, int d) {
+  if (!a.out_packed) return hq * a.D + d;
+  const int64_t b = hq / a.H;
+  return packed_index(b, (hq - b * a.H) * a.D + d, a.H * a.D);
+}
+
 // LAYER: q (and the decoded token's k, v) come from the bf16 QKV projection
 // row a.qkv + b*a.qkv_bs, columns [q | k | v]; q and k get the per-head
 // RMSNorm and RoPE at position kv_len - 1.  The unit's first block writes
@@ -373,7 +381,7 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
     }
     const int64_t hq = b * a.H + h0 + h;
     if (nsplit == 1) {
-      a.Out[hq * D + d] = f2bf(lv > 0.f ? ov / lv : 0.f);
+      a.Out[out_index(a, hq, d)] = f2bf(lv > 0.f ? ov / lv : 0.f);
     } else {
       opart[(hq * nsplit + split) * D + d] = ov;
       if (d == 0) *reinterpret_cast<float2*>(ml + (hq * nsplit + split) * 2) = make_float2(M, lv);
@@ -411,7 +419,7 @@ __global__ __launch_bounds__(D) void attn_combine_kernel(AttnArgs a, int nsplit,
     const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), s));
     acc = fmaf(w, v[s], acc);  // v[s] = 0 and w = 0 for s >= nsplit
   }
-  a.Out[hq * D + d] = f2bf(acc);
+  a.Out[out_index(a, hq, d)] = f2bf(acc);
 }
 
 int num_cus() {

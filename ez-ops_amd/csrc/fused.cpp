@@ -31,33 +31,40 @@ struct Carve {
   }
 };
 
+// Batched (B > 4) stages hand activations to the next MFMA GEMM in its
+// packed operand layout when the width allows it.
+bool packable(int64_t B, int64_t K) { return B > 4 && K % 32 == 0; }
+
 size_t ffn_ws(int64_t B, int64_t HS, int64_t IS) {
-  return align256(size_t(B * HS) * 2) * 2 + align256(size_t(B * IS) * 2);
+  const int64_t Bp = packed_rows(B);
+  return align256(size_t(B * HS) * 2) + align256(size_t(Bp * IS) * 2) + align256(size_t(Bp * HS) * 2);
 }
 
-int run_ffn(const uint16_t* attn, const uint16_t* residual, const uint16_t* Wo, const uint16_t* post_w,
-            const uint16_t* Wg, const uint16_t* Wu, const uint16_t* Wd, uint16_t* out, int64_t B,
-            int64_t HS, int64_t IS, int64_t QR, float eps, char* ws, hipStream_t s) {
+// attn_packed: `attn` is in the packed layout (the layer's attention output).
+int run_ffn(const uint16_t* attn, bool attn_packed, const uint16_t* residual, const uint16_t* Wo,
+            const uint16_t* post_w, const uint16_t* Wg, const uint16_t* Wu, const uint16_t* Wd, uint16_t* out,
+            int64_t B, int64_t HS, int64_t IS, int64_t QR, float eps, char* ws, hipStream_t s) {
   Carve c{ws};
   uint16_t* x2 = c.take<uint16_t>(size_t(B * HS) * 2);
-  uint16_t* h = c.take<uint16_t>(size_t(B * IS) * 2);
-  uint16_t* xn = c.take<uint16_t>(size_t(B * HS) * 2);  // staged RMSNorm input (batch > 4)
+  uint16_t* h = c.take<uint16_t>(size_t(packed_rows(B) * IS) * 2);
+  uint16_t* xn = c.take<uint16_t>(size_t(packed_rows(B) * HS) * 2);  // staged RMSNorm input (batch > 4)
+  const bool hp = packable(B, IS);
 
   LinearArgs o{};
-  o.X = attn; o.ldx = QR; o.W = Wo; o.Y = x2; o.ldy = HS;
+  o.X = attn; o.ldx = QR; o.x_packed = attn_packed; o.W = Wo; o.Y = x2; o.ldy = HS;
   o.M = B; o.N = HS; o.K = QR; o.res = residual; o.ldr = HS; o.epi = kEpiResid;
   int rc = launch_linear(o, s);
   if (rc) return rc;
 
   LinearArgs gu{};
-  gu.X = x2; gu.ldx = HS; gu.W = Wg; gu.W2 = Wu; gu.Y = h; gu.ldy = IS;
+  gu.X = x2; gu.ldx = HS; gu.W = Wg; gu.W2 = Wu; gu.Y = h; gu.ldy = IS; gu.y_packed = hp;
   gu.M = B; gu.N = IS; gu.K = HS; gu.norm = 1; gu.norm_w = post_w; gu.eps = eps; gu.epi = kEpiSilu;
   gu.xn_ws = xn;
   rc = launch_linear(gu, s);
   if (rc) return rc;
 
   LinearArgs dn{};
-  dn.X = h; dn.ldx = IS; dn.W = Wd; dn.Y = out; dn.ldy = HS;
+  dn.X = h; dn.ldx = IS; dn.x_packed = hp; dn.W = Wd; dn.Y = out; dn.ldy = HS;
   dn.M = B; dn.N = HS; dn.K = IS; dn.res = x2; dn.ldr = HS; dn.epi = kEpiResid;
   return launch_linear(dn, s);
 }
@@ -79,7 +86,7 @@ extern "C" int ezops_o_proj_ffn_bf16(const void* attn, const void* residual, con
   EZ_REQUIRE(attn && residual && Wo && Wg && Wu && Wd && out && ws, "o_proj_ffn: null pointer");
   EZ_REQUIRE(B >= 1 && HS >= 1 && IS >= 1 && QR >= 1, "o_proj_ffn: bad shape");
   EZ_REQUIRE(ws_bytes >= ffn_ws(B, HS, IS), "o_proj_ffn: workspace too small");
-  return run_ffn(static_cast<const uint16_t*>(attn), static_cast<const uint16_t*>(residual),
+  return run_ffn(static_cast<const uint16_t*>(attn), false, static_cast<const uint16_t*>(residual),
                  static_cast<const uint16_t*>(Wo), static_cast<const uint16_t*>(post_norm_w),
                  static_cast<const uint16_t*>(Wg), static_cast<const uint16_t*>(Wu),
                  static_cast<const uint16_t*>(Wd), static_cast<uint16_t*>(out), B, HS, IS, QR, eps,
@@ -89,9 +96,10 @@ extern "C" int ezops_o_proj_ffn_bf16(const void* attn, const void* residual, con
 namespace {
 size_t multi_kernel_ws(const ezops_qwen3_layer* p) {
   const int64_t QR = p->H * p->D, KVR = p->Hkv * p->D;
-  return align256(size_t(p->B * p->HS) * 2)            // staged RMSNorm input (batch > 4)
+  const int64_t Bp = packed_rows(p->B);
+  return align256(size_t(Bp * p->HS) * 2)                // staged RMSNorm input (batch > 4)
          + align256(size_t(p->B * (QR + 2 * KVR)) * 2)   // qkv
-         + align256(size_t(p->B * QR) * 2)              // attention output
+         + align256(size_t(Bp * QR) * 2)                 // attention output
          + align256(attn_workspace_size(p->B, p->H, p->Hkv, p->S, p->D)) + ffn_ws(p->B, p->HS, p->IS);
 }
 }  // namespace
@@ -113,9 +121,10 @@ extern "C" int ezops_qwen3_dense_decode_bf16(const ezops_qwen3_layer* p, void* w
   EZ_REQUIRE(ws_bytes >= ezops_qwen3_layer_workspace_size(p), "qwen3_dense_decode: workspace too small");
   const int64_t QR = p->H * p->D, KVR = p->Hkv * p->D, QKV = QR + 2 * KVR;
   Carve c{static_cast<char*>(ws)};
-  uint16_t* xn = c.take<uint16_t>(size_t(p->B * p->HS) * 2);
+  uint16_t* xn = c.take<uint16_t>(size_t(packed_rows(p->B) * p->HS) * 2);
   uint16_t* qkv = c.take<uint16_t>(size_t(p->B * QKV) * 2);
-  uint16_t* att = c.take<uint16_t>(size_t(p->B * QR) * 2);
+  uint16_t* att = c.take<uint16_t>(size_t(packed_rows(p->B) * QR) * 2);
+  const bool att_packed = packable(p->B, QR);
   char* attn_ws = c.take<char>(attn_workspace_size(p->B, p->H, p->Hkv, p->S, p->D));
   char* ffn = c.p;
 
@@ -134,6 +143,7 @@ extern "C" int ezops_qwen3_dense_decode_bf16(const ezops_qwen3_layer* p, void* w
   a.K = static_cast<const uint16_t*>(p->K_cache);
   a.V = static_cast<const uint16_t*>(p->V_cache);
   a.Out = att;
+  a.out_packed = att_packed;
   a.B = p->B; a.H = p->H; a.Hkv = p->Hkv; a.S = p->S; a.D = p->D;
   a.kv_lens = p->kv_lens;
   a.Lh = p->max_kv_len;
@@ -148,7 +158,7 @@ extern "C" int ezops_qwen3_dense_decode_bf16(const ezops_qwen3_layer* p, void* w
   if (rc) return rc;
 
   const uint16_t* Wgu = static_cast<const uint16_t*>(p->Wgu);
-  return run_ffn(att, hidden, static_cast<const uint16_t*>(p->Wo), static_cast<const uint16_t*>(p->post_norm_w),
+  return run_ffn(att, att_packed, hidden, static_cast<const uint16_t*>(p->Wo), static_cast<const uint16_t*>(p->post_norm_w),
                  Wgu, Wgu + p->IS * p->HS, static_cast<const uint16_t*>(p->Wd), static_cast<uint16_t*>(p->out),
                  p->B, p->HS, p->IS, QR, p->eps, ffn, s);
 }

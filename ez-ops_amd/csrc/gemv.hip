@@ -44,7 +44,7 @@ __device__ __forceinline__ void store_out(const LinearArgs& a, int64_t m, int64_
     reinterpret_cast<float*>(a.Y)[m * a.ldy + n] = v;
     return;
   }
-  uint16_t* y = reinterpret_cast<uint16_t*>(a.Y) + m * a.ldy + n;
+  uint16_t* y = reinterpret_cast<uint16_t*>(a.Y) + (a.y_packed ? packed_index(m, n, a.ldy) : m * a.ldy + n);
   if (a.epi == kEpiStore) {
     *y = f2bf(v);
   } else if (a.epi == kEpiResid) {
@@ -274,11 +274,18 @@ __global__ __launch_bounds__(mfma_waves(T) * kWave) void linear_mfma_kernel(Line
       }
   };
   // Unconditional loads from clamped addresses: no branch around a pending load.
+  // Packed X: the fragment of (batch block, k-step) is 1 KiB at a fixed place.
+  const uint16_t* xpk = a.X + int64_t(blockIdx.y) * (a.K >> 5) * 512 + lane * 8;
   auto xload = [&](int64_t c, u32x4v_t (&x)[kMfmaSteps]) {
 #pragma unroll
     for (int s = 0; s < kMfmaSteps; ++s) {
       const int64_t k = c * kMfmaKC + 32 * s + 8 * g;
-      x[s] = *reinterpret_cast<const u32x4v_t*>(xrow + (k < a.K ? k : 0));
+      if (a.x_packed) {
+        const int64_t ks = c * kMfmaSteps + s;
+        x[s] = *reinterpret_cast<const u32x4v_t*>(xpk + (k < a.K ? ks : 0) * 512);
+      } else {
+        x[s] = *reinterpret_cast<const u32x4v_t*>(xrow + (k < a.K ? k : 0));
+      }
     }
   };
 
@@ -609,9 +616,14 @@ int launch_linear(const LinearArgs& a, hipStream_t s) {
   EZ_REQUIRE(a.epi != kEpiSilu || a.W2, "linear: SwiGLU epilogue needs the up-projection weights");
   EZ_REQUIRE(a.epi != kEpiResid || a.res, "linear: residual epilogue needs the residual");
   EZ_REQUIRE(a.N < (int64_t(1) << 31) / 16 && a.M < 65536 * 16, "linear: sizes too large");
+  EZ_REQUIRE(!(a.x_packed || a.y_packed) || a.M > 4, "linear: the packed layouts are for M > 4");
+  EZ_REQUIRE(!a.x_packed || a.K % 32 == 0, "linear: packed X needs K %% 32 == 0");
+  EZ_REQUIRE(!a.y_packed || (a.N % 32 == 0 && a.ldy == a.N && a.epi != kEpiStoreF32),
+             "linear: packed Y needs N %% 32 == 0, ldy == N and a bf16 epilogue");
   const bool silu = a.epi == kEpiSilu;
   const bool vec = (a.K % 8 == 0) && (a.ldx % 8 == 0) && aligned16(a.X) && aligned16(a.W) &&
                    (!silu || aligned16(a.W2)) && (!a.norm_w || aligned16(a.norm_w));
+  EZ_REQUIRE(vec || !(a.x_packed || a.y_packed), "linear: the packed layouts need 16-byte aligned operands");
   if (!vec) {
     const int64_t blocks = (a.N + kWavesPerBlock - 1) / kWavesPerBlock;
     hipLaunchKernelGGL(linear_scalar_kernel, dim3(blocks), dim3(kBlock), 0, s, a);
@@ -628,11 +640,18 @@ int launch_linear(const LinearArgs& a, hipStream_t s) {
     // work in every block of 16 weight rows: measured slower than staging.)
     LinearArgs b = a;
     if (a.norm) {
-      EZ_REQUIRE(a.xn_ws, "linear: RMSNorm prologue with M > 4 needs a workspace of M*K bf16");
-      EZ_REQUIRE(a.ldx == a.K, "linear: RMSNorm prologue with M > 4 needs contiguous X rows");
-      const int rc = ezops_rmsnorm_bf16(a.X, a.norm_w, a.xn_ws, a.M, a.K, a.eps, s);
+      EZ_REQUIRE(a.xn_ws, "linear: RMSNorm prologue with M > 4 needs a workspace (ezops_linear_stage_workspace_size)");
+      EZ_REQUIRE(!a.x_packed && a.ldx == a.K, "linear: RMSNorm prologue with M > 4 needs contiguous X rows");
+      int rc;
+      if (a.K % 32 == 0) {  // staged straight into the MFMA-packed layout
+        rc = launch_rmsnorm_bf16_packed(a.X, a.norm_w, a.xn_ws, a.M, a.K, a.eps, s);
+        b.x_packed = 1;
+      } else {
+        rc = ezops_rmsnorm_bf16(a.X, a.norm_w, a.xn_ws, a.M, a.K, a.eps, s);
+      }
       if (rc) return rc;
       b.X = a.xn_ws;
+      b.ldx = a.K;
       b.norm = 0;
     }
     silu ? launch_mfma<true>(b, s) : launch_mfma<false>(b, s);
@@ -674,7 +693,7 @@ extern "C" int ezops_linear_bf16(const void* X, int64_t ldx, const void* W, void
 }
 
 extern "C" size_t ezops_linear_stage_workspace_size(int64_t M, int64_t K, int norm) {
-  return (norm && M > 4) ? size_t(M * K) * 2 : 0;
+  return (norm && M > 4) ? size_t(ez::packed_rows(M) * K) * 2 : 0;
 }
 
 extern "C" int ezops_linear_stage_bf16(const void* X, int64_t ldx, const void* W, const void* W2, void* Y,

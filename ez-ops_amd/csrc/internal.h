@@ -8,6 +8,16 @@
 
 namespace ez {
 
+// "MFMA-packed" activation layout for the skinny GEMM (M > 4): batch rows
+// in blocks of 16, each 32-wide k-step of a block stored as the 1 KiB B
+// operand of v_mfma_f32_16x16x32_bf16 (lane 16 g + i holds row i, k-slots
+// 8 g .. 8 g + 7), so every fragment load is one contiguous 1 KiB read.
+// Element (m, k) of an [M, K] matrix (K % 32 == 0; M padded to 16) sits at:
+__host__ __device__ __forceinline__ int64_t packed_index(int64_t m, int64_t k, int64_t K) {
+  return (((m >> 4) * (K >> 5) + (k >> 5)) * 64 + ((k >> 3) & 3) * 16 + (m & 15)) * 8 + (k & 7);
+}
+__host__ __device__ __forceinline__ int64_t packed_rows(int64_t M) { return (M + 15) / 16 * 16; }
+
 enum Epilogue : int {
   kEpiStore = 0,   // Y = bf16(acc)
   kEpiResid = 1,   // Y = bf16(res + bf16(acc))            (o_proj / down_proj + residual)
@@ -29,10 +39,17 @@ struct LinearArgs {
   const uint16_t* norm_w;      // NULL = unit weight
   float eps;
   int epi;
-  uint16_t* xn_ws;             // M > 4 with `norm`: M*K bf16 scratch for the staged input
+  uint16_t* xn_ws;             // M > 4 with `norm`: packed_rows(M)*K bf16 scratch for the staged input
+  int x_packed;                // X is in the MFMA-packed layout (M > 4, K % 32 == 0; ldx unused)
+  int y_packed;                // Y is written in the MFMA-packed layout (M > 4, ldy = N, N % 32 == 0)
 };
 
 int launch_linear(const LinearArgs& a, hipStream_t s);
+
+// Out = bf16(X * rsqrt(mean(X^2) + eps) * W) per row, written in the
+// MFMA-packed layout (rowops.hip); dim % 32 == 0, Out holds packed_rows(rows)*dim.
+int launch_rmsnorm_bf16_packed(const uint16_t* X, const uint16_t* W, uint16_t* Out, int64_t rows, int64_t dim,
+                               float eps, hipStream_t s);
 
 struct QkRopeArgs {
   const uint16_t* q; int64_t q_bs;
@@ -54,6 +71,7 @@ struct AttnArgs {
   uint16_t* Out;      // [B, H, D]
   int64_t B, H, Hkv, S, D;
   const int32_t* kv_lens;
+  int out_packed;     // Out in the MFMA-packed layout of [B, H*D] (the layer's o_proj input)
   int64_t Lh;         // bound on the live lengths for planning (0 = S); lengths above it are cut to it
   float scale;
   // Fused layer prologue (Q == NULL): q/k/v of the decoded token come from

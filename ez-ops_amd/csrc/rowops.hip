@@ -59,8 +59,9 @@ __global__ __launch_bounds__(256) void rmsnorm_f32_loop_kernel(const float* __re
 }
 
 // ------------------------------------------------------ RMSNorm bf16 + weight
-// One block per row; VPT chunks of 8 bf16 per thread.
-template <int BS, int VPT>
+// One block per row; VPT chunks of 8 bf16 per thread.  PACKED writes the
+// row into the MFMA-packed layout of the skinny GEMM (dim % 32 == 0).
+template <int BS, int VPT, bool PACKED = false>
 __global__ __launch_bounds__(BS) void rmsnorm_bf16_reg_kernel(const uint16_t* __restrict__ X,
                                                                const uint16_t* __restrict__ W,
                                                                uint16_t* __restrict__ Out,
@@ -69,14 +70,21 @@ __global__ __launch_bounds__(BS) void rmsnorm_bf16_reg_kernel(const uint16_t* __
   const int64_t row = blockIdx.x;
   const uint4* x = reinterpret_cast<const uint4*>(X + row * dim);
   const uint4* w = reinterpret_cast<const uint4*>(W);
-  uint4* o = reinterpret_cast<uint4*>(Out + row * dim);
+  uint4* o = reinterpret_cast<uint4*>(Out + row * dim);  // row-major output
   const int64_t n8 = dim >> 3;
-  uint4 v[VPT];
+  uint4 v[VPT], wv[VPT];
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
     const int64_t c = threadIdx.x + int64_t(j) * BS;
     v[j] = c < n8 ? x[c] : make_uint4(0, 0, 0, 0);
+  }
+  // The weight pieces are requested with the row, not after the reduction.
+  constexpr uint32_t one2 = 0x3f803f80u;  // two bf16 1.0
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int64_t c = threadIdx.x + int64_t(j) * BS;
+    wv[j] = (W && c < n8) ? w[c] : make_uint4(one2, one2, one2, one2);
   }
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
@@ -93,14 +101,11 @@ __global__ __launch_bounds__(BS) void rmsnorm_bf16_reg_kernel(const uint16_t* __
     if (c < n8) {
       float f[8], g[8];
       unpack8(v[j], f);
-      if (W) {
-        unpack8(w[c], g);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) g[e] = 1.f;
-      }
-      o[c] = make_uint4(pack_bf2(f[0] * r * g[0], f[1] * r * g[1]), pack_bf2(f[2] * r * g[2], f[3] * r * g[3]),
-                        pack_bf2(f[4] * r * g[4], f[5] * r * g[5]), pack_bf2(f[6] * r * g[6], f[7] * r * g[7]));
+      unpack8(wv[j], g);
+      const uint4 y = make_uint4(pack_bf2(f[0] * r * g[0], f[1] * r * g[1]), pack_bf2(f[2] * r * g[2], f[3] * r * g[3]),
+                                 pack_bf2(f[4] * r * g[4], f[5] * r * g[5]), pack_bf2(f[6] * r * g[6], f[7] * r * g[7]));
+      if constexpr (PACKED) *reinterpret_cast<uint4*>(Out + packed_index(row, 8 * c, dim)) = y;
+      else o[c] = y;
     }
   }
 }
@@ -310,15 +315,15 @@ void launch_rms_f32(const float* X, float* O, int64_t rows, int64_t dim, float e
   else hipLaunchKernelGGL((rmsnorm_f32_reg_kernel<BS, 8>), g, b, 0, s, X, O, dim, eps);
 }
 
-template <int BS>
+template <int BS, bool PACKED = false>
 void launch_rms_bf16(const uint16_t* X, const uint16_t* W, uint16_t* O, int64_t rows, int64_t dim,
                      float eps, hipStream_t s) {
   const int64_t vpt = (dim / 8 + BS - 1) / BS;
   const dim3 g{unsigned(rows), 1, 1}, b{unsigned(BS), 1, 1};
-  if (vpt <= 1) hipLaunchKernelGGL((rmsnorm_bf16_reg_kernel<BS, 1>), g, b, 0, s, X, W, O, dim, eps);
-  else if (vpt <= 2) hipLaunchKernelGGL((rmsnorm_bf16_reg_kernel<BS, 2>), g, b, 0, s, X, W, O, dim, eps);
-  else if (vpt <= 4) hipLaunchKernelGGL((rmsnorm_bf16_reg_kernel<BS, 4>), g, b, 0, s, X, W, O, dim, eps);
-  else hipLaunchKernelGGL((rmsnorm_bf16_reg_kernel<BS, 8>), g, b, 0, s, X, W, O, dim, eps);
+  if (vpt <= 1) hipLaunchKernelGGL((rmsnorm_bf16_reg_kernel<BS, 1, PACKED>), g, b, 0, s, X, W, O, dim, eps);
+  else if (vpt <= 2) hipLaunchKernelGGL((rmsnorm_bf16_reg_kernel<BS, 2, PACKED>), g, b, 0, s, X, W, O, dim, eps);
+  else if (vpt <= 4) hipLaunchKernelGGL((rmsnorm_bf16_reg_kernel<BS, 4, PACKED>), g, b, 0, s, X, W, O, dim, eps);
+  else hipLaunchKernelGGL((rmsnorm_bf16_reg_kernel<BS, 8, PACKED>), g, b, 0, s, X, W, O, dim, eps);
 }
 
 template <int BS>
@@ -363,7 +368,7 @@ extern "C" int ezops_rmsnorm_bf16(const void* Xv, const void* Wv, void* Ov, int6
   const bool vec = dim % 8 == 0 && aligned16(X) && aligned16(O) && (!W || aligned16(W));
   if (!vec || dim > 65536) {
     hipLaunchKernelGGL(rmsnorm_bf16_loop_kernel, dim3(unsigned(rows)), dim3(256), 0, s, X, W, O, dim, eps);
-  } else if (dim <= 4096) {
+  } else if (dim <= 1024) {
     launch_rms_bf16<64>(X, W, O, rows, dim, eps, s);
   } else if (dim <= 16384) {
     launch_rms_bf16<256>(X, W, O, rows, dim, eps, s);
@@ -372,6 +377,18 @@ extern "C" int ezops_rmsnorm_bf16(const void* Xv, const void* Wv, void* Ov, int6
   }
   return launch_status("rmsnorm_bf16");
 }
+
+namespace ez {
+int launch_rmsnorm_bf16_packed(const uint16_t* X, const uint16_t* W, uint16_t* O, int64_t rows, int64_t dim,
+                               float eps, hipStream_t s) {
+  EZ_REQUIRE(X && O, "rmsnorm_bf16_packed: null pointer");
+  EZ_REQUIRE(rows >= 1 && dim >= 32 && dim % 32 == 0 && dim <= 16384 && aligned16(X) && aligned16(O) &&
+                 (!W || aligned16(W)),
+             "rmsnorm_bf16_packed: needs aligned rows, dim %% 32 == 0 and dim <= 16384");
+  launch_rms_bf16<256, true>(X, W, O, rows, dim, eps, s);
+  return launch_status("rmsnorm_bf16_packed");
+}
+}  // namespace ez
 
 extern "C" int ezops_softmax_f32(const float* X, float* Out, int64_t rows, int64_t dim, hipStream_t s) {
   EZ_REQUIRE(X && Out, "softmax_f32: null pointer");
