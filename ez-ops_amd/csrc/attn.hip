@@ -130,6 +130,22 @@ __device__ __forceinline__ int64_t out_index(const AttnArgs& a, int64_t hq, int 
   return packed_index(b, (hq - b * a.H) * a.D + d, a.H * a.D);
 }
 
+// Longest-first order of ragged batches: blocks are dispatched in index
+// order, so rank r of the grid serves the r-th longest sequence (ties by
+// index) and the long sequences never start last.  One wave, B <= 64: lane j
+// ranks sequence j against all others, the lane holding rank r is found by
+// ballot.
+__device__ __forceinline__ int rank_to_seq(const int32_t* lens, int B, int r, int lane) {
+  const int32_t Lj = lane < B ? lens[lane] : -1;
+  int rank = 0;
+  for (int j = 0; j < B; ++j) {
+    const int32_t Lo = __builtin_amdgcn_readlane(Lj, j);
+    rank += (Lo > Lj) || (Lo == Lj && j < lane);
+  }
+  const uint64_t hit = __ballot(lane < B && rank == r);
+  return hit ? __ffsll(static_cast<unsigned long long>(hit)) - 1 : r;
+}
+
 // LAYER: q (and the decoded token's k, v) come from the bf16 QKV projection
 // row a.qkv + b*a.qkv_bs, columns [q | k | v]; q and k get the per-head
 // RMSNorm and RoPE at position kv_len - 1.  The unit's first block writes
@@ -156,7 +172,9 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
   EZ_TRACE(0);
   const int li = lane & 15, lg = lane >> 4;
   const int dc = lane % CPR, rs = lane / CPR;
-  const int kvh = unit % int(a.Hkv), b = unit / int(a.Hkv);
+  const int kvh = unit % int(a.Hkv);
+  int b = unit / int(a.Hkv);
+  if (a.sort_lens) b = rank_to_seq(a.kv_lens, int(a.B), b, lane);
   // The length is requested first, ahead of this wave's tile loads, and
   // unconditionally (a dummy address without kv_lens), so that nothing waits
   // for it before its first use.
@@ -499,6 +517,7 @@ int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
   EZ_REQUIRE(a.Lh >= 0, "attn_decode: max_kv_len must be >= 0");
   AttnArgs aa = a;
   aa.Lh = (a.Lh == 0 || a.Lh > a.S || !a.kv_lens) ? a.S : a.Lh;
+  aa.sort_lens = a.kv_lens && a.B > 1 && a.B <= kWave;
   if (aa.scale <= 0.f) aa.scale = 1.0f / sqrtf(float(a.D));
   const SplitPlan pl = plan_splits(aa.B, aa.Hkv, aa.Lh, G);
   float *opart = nullptr, *ml = nullptr;
