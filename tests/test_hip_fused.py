@@ -118,3 +118,32 @@ def test_qwen3_layer_repeated_calls():
                                        in_norm_w=npy[7], q_norm_w=npy[8], k_norm_w=npy[9], post_norm_w=npy[10],
                                        cos=npy[11], sin=npy[12])
         assert op.check(out, torch.from_numpy(ref).to(out.device)), it
+
+
+@pytest.mark.parametrize("batch", [1, 16])
+def test_qwen3_layer_graph_replays(batch):
+    """The layer captured once in a HIP graph and replayed: every replay equals
+    the eager result (split partials, merge counters and cache slots return to
+    their start state within each call)."""
+    torch.manual_seed(9)
+    rng = np.random.default_rng(9)
+    lens = rng.integers(1024, 4096 + 1, size=batch).tolist()
+    op = Qwen3DenseDecodeOp(batch, 4096, backend="hip", kv_lens=lens, norm_weights=True, rope_theta=1e6,
+                            **QWEN3_8B, num_kv_heads=8)
+    data = op.gen_data()
+    eager = op(*data).clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        op(*data)  # warm the workspace on this stream
+        g_ = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_, stream=s):
+            out = op(*data)
+    torch.cuda.current_stream().wait_stream(s)
+    for _ in range(4):
+        g_.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        eager2 = op(*data)  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(eager2, eager)
