@@ -157,7 +157,8 @@ def op_table(torch, _hip, flush, peak_gbps: float) -> dict:
     inputs are large; the per-launch time is the replay time / launches (median
     of 10 flushed replays), so the graph-launch latency is amortised.
     """
-    from ezops import AttnDecodeOp, FusedOProjFfnOp, FusedQkNormRopeOp, GemvOp, ReduceOp, RmsNormOp, SoftmaxOp
+    from ezops import (AttnDecodeOp, FusedOProjFfnOp, FusedQkNormRopeOp, GemvOp, PagedAttnDecodeOp, ReduceOp,
+                       RmsNormOp, SoftmaxOp)
 
     out = {}
     gcu = torch.Generator(device="cuda")
@@ -207,6 +208,15 @@ def op_table(torch, _hip, flush, peak_gbps: float) -> dict:
     at = AttnDecodeOp(32, 32, 8192, 128, backend="hip", num_kv_heads=8)
     rec("gqa_decode_b32_h32_kv8_s8192", lambda i: at(Q, K, V), 1_074_266_112, 3)
     del K, V
+    torch.cuda.empty_cache()
+    # the same workload over a paged cache: 64-row pages dealt to the
+    # sequences in a random order (4096 pages of 32 x 8 x 64 x 128 bf16)
+    Kp, Vp = randn(4096, 8, 64, 128), randn(4096, 8, 64, 128)
+    bt = torch.randperm(4096, generator=gcu, device="cuda").to(torch.int32).reshape(32, 128)
+    lens = torch.full((32,), 8192, dtype=torch.int32, device="cuda")
+    pat = PagedAttnDecodeOp(32, 32, 8, 128, page_size=64, max_pages=128, backend="hip")
+    rec("paged_gqa_decode_b32_h32_kv8_s8192_p64", lambda i: pat(Q, Kp, Vp, bt, lens, 8192), 1_074_266_112 + 16_384 + 128, 3)
+    del Kp, Vp
     torch.cuda.empty_cache()
 
     for B in (1, 16):

@@ -56,15 +56,58 @@ __device__ long long ez_attn_trace[65536 * 8];  // [block][wave][8] s_memrealtim
   } while (0)
 #endif
 
-// K tile rows t0 + 16u + li (clamped to `last`) into the MFMA B operand.
+// Where the cache rows of one (sequence, kv head) unit live.  Contiguous:
+// one S x D slab.  Paged: page j of the sequence is pool page bt[j], each
+// pool page holding [Hkv][P][D]; P is a multiple of the 32-row tile, so a
+// tile never crosses a page and one table lookup serves a whole tile.
+template <int D, bool PAGED>
+struct KvRows {
+  const uint16_t* base;   // contiguous: the unit's slab; paged: the pool
+  const int32_t* bt;      // paged: the sequence's block-table row
+  int64_t head_off;       // paged: kv head offset inside a page (elements)
+  int64_t page_elems;     // paged: Hkv * P * D
+  int page_shift;         // paged: log2(P)
+  uint32_t last_page;     // paged: pool pages - 1 (ids are clamped into the pool)
+  int64_t last_entry;     // paged: block-table row length - 1
+
+  // Block-table entry of the page holding row ts, as a vector load (lane 0
+  // reads it; odd lanes read the next entry, clamped to the row) so that its
+  // wait is ordered with the tile loads rather than the LDS traffic.
+  __device__ __forceinline__ int32_t page_id(int64_t ts, int lane) const {
+    if constexpr (!PAGED) return 0;
+    int64_t e = (ts >> page_shift) + (lane & 1);
+    e = e < last_entry ? e : last_entry;
+    return bt[e];
+  }
+  // First row of the tile starting at row ts, given page_id(ts) (any lane's
+  // copy from lane 0).
+  __device__ __forceinline__ const uint16_t* at(int64_t ts, int32_t id_v) const {
+    if constexpr (!PAGED) return base + ts * D;
+    const uint32_t id = min(uint32_t(__builtin_amdgcn_readfirstlane(id_v)), last_page);
+    return base + int64_t(id) * page_elems + head_off + (ts & ((int64_t(1) << page_shift) - 1)) * D;
+  }
+  __device__ __forceinline__ const uint16_t* tile(int64_t ts) const {
+    if constexpr (!PAGED) return base + ts * D;
+    return at(ts, bt[ts >> page_shift]);
+  }
+};
+
+// First row of the tile holding rows t0 + r clamped to `last` (a clamped
+// tile starts at the tile of `last`).
+__device__ __forceinline__ int64_t tile_start(int64_t t0, int64_t last) {
+  return t0 <= last ? t0 : (last & ~int64_t(kTile - 1));
+}
+
+// K tile rows t0 + 16u + li (clamped to `last`) into the MFMA B operand;
+// tb is the first row of the tile at ts = tile_start(t0, last).
 template <int D, int NSUB>
-__device__ __forceinline__ void load_k_tile(const uint16_t* Kb, int64_t t0, int64_t last, int li, int lg,
-                                            uint4 (&kf)[NSUB][D / 32]) {
+__device__ __forceinline__ void load_k_tile(const uint16_t* tb, int64_t ts, int64_t t0, int64_t last, int li,
+                                            int lg, uint4 (&kf)[NSUB][D / 32]) {
 #pragma unroll
   for (int u = 0; u < NSUB; ++u) {
     int64_t p = t0 + 16 * u + li;
     p = p < last ? p : last;
-    const uint16_t* row = Kb + p * D + lg * 8;
+    const uint16_t* row = tb + (p - ts) * D + lg * 8;
 #pragma unroll
     for (int s = 0; s < D / 32; ++s) kf[u][s] = ld16_stream(row + 32 * s);
   }
@@ -73,14 +116,14 @@ __device__ __forceinline__ void load_k_tile(const uint16_t* Kb, int64_t t0, int6
 // V rows in row layout: lane (dc, rs) reads rows rs, rs + RPI, ... of the
 // tile (clamped to `last`), 16 B at column 8*dc.
 template <int D, int NPV>
-__device__ __forceinline__ void load_v_tile(const uint16_t* Vb, int64_t t0, int64_t last, int dc, int rs,
-                                            uint4 (&vf)[NPV]) {
+__device__ __forceinline__ void load_v_tile(const uint16_t* tb, int64_t ts, int64_t t0, int64_t last, int dc,
+                                            int rs, uint4 (&vf)[NPV]) {
   constexpr int RPI = kWave / (D / 8);
 #pragma unroll
   for (int j = 0; j < NPV; ++j) {
     int64_t p = t0 + rs + RPI * j;
     p = p < last ? p : last;
-    vf[j] = ld16_stream(Vb + p * D + dc * 8);
+    vf[j] = ld16_stream(tb + (p - ts) * D + dc * 8);
   }
 }
 
@@ -151,7 +194,9 @@ __device__ __forceinline__ int rank_to_seq(const int32_t* lens, int B, int r, in
 // RMSNorm and RoPE at position kv_len - 1.  The unit's first block writes
 // the token's k, v into the cache slot; no block reads that slot: the token
 // enters the softmax as a virtual row from LDS (wave 0 of split 0).
-template <int D, int G, int W, bool LAYER>
+//
+// PAGED: the cache is a page pool addressed through a.block_table (see KvRows).
+template <int D, int G, int W, bool LAYER, bool PAGED>
 __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int nsplit, float* opart, float* ml) {
   constexpr int NS = D / 32;         // MFMA k-steps per 16-position sub-tile
   constexpr int CPR = D / 8;         // 16-byte chunks per K/V row
@@ -179,8 +224,18 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
   // unconditionally (a dummy address without kv_lens), so that nothing waits
   // for it before its first use.
   const int32_t Lraw = *(a.kv_lens ? a.kv_lens + b : reinterpret_cast<const int32_t*>(a.K));
-  const uint16_t* Kb = a.K + (int64_t(b) * a.Hkv + kvh) * a.S * D;
-  const uint16_t* Vb = a.V + (int64_t(b) * a.Hkv + kvh) * a.S * D;
+  KvRows<D, PAGED> kr{}, vr{};
+  if constexpr (PAGED) {
+    const int32_t* bt = a.block_table + int64_t(b) * a.bt_stride;
+    const int64_t pe = a.Hkv * a.page_size * D, ho = int64_t(kvh) * a.page_size * D;
+    const int sh = __builtin_ctz(unsigned(a.page_size));
+    const uint32_t lp = uint32_t(a.num_pages - 1);
+    kr = {a.K, bt, ho, pe, sh, lp, a.bt_stride - 1};
+    vr = {a.V, bt, ho, pe, sh, lp, a.bt_stride - 1};
+  } else {
+    kr.base = a.K + (int64_t(b) * a.Hkv + kvh) * a.S * D;
+    vr.base = a.V + (int64_t(b) * a.Hkv + kvh) * a.S * D;
+  }
   const int64_t h0 = int64_t(kvh) * G;  // first query head of the group
   const float sl2 = a.scale * kLog2e;
   const int64_t stride = int64_t(nsplit) * W * kTile;  // distance between a wave's tiles
@@ -188,8 +243,12 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
   int64_t t0 = (int64_t(split) * W + wave) * kTile;
   uint4 kf[NSUB][NS], vf[NPV];
   __builtin_amdgcn_sched_barrier(0);
-  load_k_tile<D, NSUB>(Kb, t0, a.Lh - 1, li, lg, kf);
-  load_v_tile<D, NPV>(Vb, t0, a.Lh - 1, dc, rs, vf);
+  {
+    const int64_t ts = tile_start(t0, a.Lh - 1);
+    const int32_t id = kr.page_id(ts, lane);
+    load_k_tile<D, NSUB>(kr.at(ts, id), ts, t0, a.Lh - 1, li, lg, kf);
+    load_v_tile<D, NPV>(vr.at(ts, id), ts, t0, a.Lh - 1, dc, rs, vf);
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   int64_t L = a.kv_lens ? int64_t(Lraw) : a.S;
@@ -198,6 +257,8 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
   // Cache rows read here: [0, Lc) (the layer's decoded token is the virtual row).
   const int64_t Lc = LAYER ? (L > 0 ? L - 1 : 0) : L;
   const int64_t cl = Lc > 0 ? Lc - 1 : 0;  // clamp row of later tiles
+  // Paged: the table entry of the next tile is read one iteration ahead.
+  int32_t id_next = kr.page_id(tile_start(t0 + stride, cl), lane);
 
   bf16x8_t qf[NS];
   if constexpr (LAYER) {
@@ -217,8 +278,9 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
     }
     __syncthreads();  // Qs, Kn, Vn complete
     if (publisher && L > 0) {
-      uint16_t* kdst = const_cast<uint16_t*>(Kb) + pos * D;
-      uint16_t* vdst = const_cast<uint16_t*>(Vb) + pos * D;
+      const int64_t ps = pos & ~int64_t(kTile - 1);
+      uint16_t* kdst = const_cast<uint16_t*>(kr.tile(ps)) + (pos - ps) * D;
+      uint16_t* vdst = const_cast<uint16_t*>(vr.tile(ps)) + (pos - ps) * D;
       for (int i = lane; i < D; i += kWave) {
         kdst[i] = Kn[i];
         vdst[i] = Vn[i];
@@ -265,7 +327,10 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
       if (acc[0][0] == 1.2345e-30f) a.Out[0] = 1;  // the stamp follows the MFMA results
       EZ_TRACE(3 + it);
     }
-    load_k_tile<D, NSUB>(Kb, tn, cl, li, lg, kf);  // next K while this tile finishes
+    const int64_t tsn = tile_start(tn, cl);
+    const int32_t id_n = id_next;
+    load_k_tile<D, NSUB>(kr.at(tsn, id_n), tsn, tn, cl, li, lg, kf);  // next K while this tile finishes
+    id_next = kr.page_id(tile_start(tn + stride, cl), lane);
 
     float mx[4];
 #pragma unroll
@@ -333,7 +398,7 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
         for (int e = 0; e < 8; ++e) o[h][e] = fmaf(pr[h], v[e], o[h][e]);
       }
     }
-    load_v_tile<D, NPV>(Vb, tn, cl, dc, rs, vf);  // next V
+    load_v_tile<D, NPV>(vr.at(tsn, id_n), tsn, tn, cl, dc, rs, vf);  // next V
     __builtin_amdgcn_wave_barrier();
   }
 
@@ -476,11 +541,11 @@ SplitPlan plan_splits(int64_t B, int64_t Hkv, int64_t Lh, int64_t G) {
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
-template <int D, bool LAYER>
+template <int D, bool LAYER, bool PAGED>
 void launch_d(const AttnArgs& a, const SplitPlan& pl, float* opart, float* ml, int64_t G, hipStream_t s) {
   const dim3 grid{unsigned(a.B * a.Hkv * pl.nsplit), 1, 1}, block{unsigned(pl.waves * kWave), 1, 1};
 #define EZ_LAUNCH(GG, WW) \
-  hipLaunchKernelGGL((attn_split_kernel<D, GG, WW, LAYER>), grid, block, 0, s, a, pl.nsplit, opart, ml)
+  hipLaunchKernelGGL((attn_split_kernel<D, GG, WW, LAYER, PAGED>), grid, block, 0, s, a, pl.nsplit, opart, ml)
   if (G == 8) {
     EZ_LAUNCH(8, 4);
   } else if (pl.waves == 8) {
@@ -515,6 +580,9 @@ int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
   EZ_REQUIRE(a.D == 64 || a.D == 128, "attn_decode: head_dim must be 64 or 128");
   EZ_REQUIRE((a.cos == nullptr) == (a.sin == nullptr), "attn_decode: cos and sin go together");
   EZ_REQUIRE(a.Lh >= 0, "attn_decode: max_kv_len must be >= 0");
+  EZ_REQUIRE(!a.block_table || (a.page_size >= kTile && (a.page_size & (a.page_size - 1)) == 0 &&
+                                a.bt_stride >= 1 && a.S == a.bt_stride * a.page_size),
+             "paged attn_decode: page_size must be a power of two >= %d and S = max_pages * page_size", kTile);
   AttnArgs aa = a;
   aa.Lh = (a.Lh == 0 || a.Lh > a.S || !a.kv_lens) ? a.S : a.Lh;
   aa.sort_lens = a.kv_lens && a.B > 1 && a.B <= kWave;
@@ -527,12 +595,23 @@ int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
     opart = static_cast<float*>(ws);
     ml = reinterpret_cast<float*>(static_cast<char*>(ws) + align256(size_t(a.B * a.H * pl.nsplit * a.D) * 4));
   }
+  const bool paged = a.block_table != nullptr;
   if (layer) {
-    if (a.D == 64) launch_d<64, true>(aa, pl, opart, ml, G, s);
-    else launch_d<128, true>(aa, pl, opart, ml, G, s);
+    if (paged) {
+      if (a.D == 64) launch_d<64, true, true>(aa, pl, opart, ml, G, s);
+      else launch_d<128, true, true>(aa, pl, opart, ml, G, s);
+    } else {
+      if (a.D == 64) launch_d<64, true, false>(aa, pl, opart, ml, G, s);
+      else launch_d<128, true, false>(aa, pl, opart, ml, G, s);
+    }
   } else {
-    if (a.D == 64) launch_d<64, false>(aa, pl, opart, ml, G, s);
-    else launch_d<128, false>(aa, pl, opart, ml, G, s);
+    if (paged) {
+      if (a.D == 64) launch_d<64, false, true>(aa, pl, opart, ml, G, s);
+      else launch_d<128, false, true>(aa, pl, opart, ml, G, s);
+    } else {
+      if (a.D == 64) launch_d<64, false, false>(aa, pl, opart, ml, G, s);
+      else launch_d<128, false, false>(aa, pl, opart, ml, G, s);
+    }
   }
   if (pl.nsplit > 1) {
     const dim3 grid{unsigned(a.B * a.H), 1, 1}, block{unsigned(a.D), 1, 1};
@@ -557,6 +636,31 @@ extern "C" int ezops_attn_trace_read(void* host, size_t bytes) {
 
 extern "C" size_t ezops_attn_decode_workspace_size(int64_t B, int64_t H, int64_t Hkv, int64_t S, int64_t D) {
   return ez::attn_workspace_size(B, H, Hkv, S, D);
+}
+
+extern "C" int ezops_paged_attn_decode_bf16(const void* Q, const void* K_pages, const void* V_pages, void* Out,
+                                            const int32_t* block_table, const int32_t* kv_lens, int64_t B, int64_t H,
+                                            int64_t Hkv, int64_t D, int64_t num_pages, int64_t page_size,
+                                            int64_t max_pages,
+                                            int64_t max_kv_len, float scale, void* ws, size_t ws_bytes,
+                                            hipStream_t stream) {
+  EZ_REQUIRE(Q && block_table && kv_lens, "paged attn_decode: null pointer");
+  EZ_REQUIRE(page_size >= 1 && max_pages >= 1 && num_pages >= 1 && num_pages <= (int64_t(1) << 31),
+             "paged attn_decode: bad page geometry");
+  ez::AttnArgs a{};
+  a.Q = static_cast<const uint16_t*>(Q);
+  a.K = static_cast<const uint16_t*>(K_pages);
+  a.V = static_cast<const uint16_t*>(V_pages);
+  a.Out = static_cast<uint16_t*>(Out);
+  a.B = B; a.H = H; a.Hkv = Hkv; a.S = max_pages * page_size; a.D = D;
+  a.kv_lens = kv_lens;
+  a.block_table = block_table;
+  a.bt_stride = max_pages;
+  a.page_size = int(page_size);
+  a.num_pages = num_pages;
+  a.Lh = max_kv_len;
+  a.scale = scale;
+  return ez::launch_attn(a, ws, ws_bytes, stream);
 }
 
 extern "C" int ezops_attn_decode_bf16(const void* Q, const void* K, const void* V, void* Out, int64_t B,

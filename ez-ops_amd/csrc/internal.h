@@ -67,7 +67,10 @@ int launch_qk_norm_rope(const QkRopeArgs& a, hipStream_t s);
 
 struct AttnArgs {
   const uint16_t* Q;  // [B, H, D]; NULL selects the fused layer prologue below
-  const uint16_t* K; const uint16_t* V;  // [B, Hkv, S, D]
+  const uint16_t* K; const uint16_t* V;  // [B, Hkv, S, D], or page pools [pages, Hkv, page_size, D]
+  // Paged cache (block_table != NULL): logical page j of sequence b is pool
+  // page block_table[b * bt_stride + j]; S = bt_stride * page_size.
+  const int32_t* block_table; int64_t bt_stride; int page_size; int64_t num_pages;
   uint16_t* Out;      // [B, H, D]
   int64_t B, H, Hkv, S, D;
   const int32_t* kv_lens;

@@ -3,6 +3,7 @@ from .base_op import Op
 from .fused_o_proj_ffn import FusedOProjFfnOp
 from .fused_qk_norm_rope import FusedQkNormRopeOp
 from .gemv import GemvOp
+from .paged_attn_decode import PagedAttnDecodeOp
 from .qwen3_dense_decode import Qwen3DenseDecodeOp
 from .reduce import ReduceOp
 from .rmsnorm import RmsNormOp
@@ -10,6 +11,6 @@ from .softmax import SoftmaxOp
 from .utils.roofline import RooflineResult
 
 __all__ = [
-    "AttnDecodeOp", "FusedOProjFfnOp", "FusedQkNormRopeOp", "GemvOp", "Op", "Qwen3DenseDecodeOp",
+    "AttnDecodeOp", "FusedOProjFfnOp", "FusedQkNormRopeOp", "GemvOp", "Op", "PagedAttnDecodeOp", "Qwen3DenseDecodeOp",
     "ReduceOp", "RmsNormOp", "RooflineResult", "SoftmaxOp",
 ]

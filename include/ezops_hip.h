@@ -114,6 +114,26 @@ int ezops_attn_decode_bf16(const void* Q, const void* K, const void* V, void* Ou
                            int64_t max_kv_len, float scale, void* workspace,
                            size_t workspace_bytes, hipStream_t stream);
 
+/* The same decode attention over a paged KV cache (block tables).
+ * K_pages / V_pages [num_pages, Hkv, page_size, D] bf16 page pools;
+ * block_table [B, max_pages] int32: logical page j of sequence b (cache rows
+ * [j*page_size, (j+1)*page_size)) is pool page block_table[b*max_pages + j].
+ * page_size a power of two >= 32.  kv_lens [B] int32 (required) and
+ * max_kv_len as in ezops_attn_decode_bf16 with S = max_pages * page_size.
+ * Only the entries below ceil(max_kv_len / page_size) are read; ids outside
+ * [0, num_pages) are clamped into the pool, never dereferenced out of it.
+ * Workspace: ezops_attn_decode_workspace_size(B, H, Hkv, max_pages*page_size, D).
+ * Results equal ezops_attn_decode_bf16 on the gathered contiguous cache.
+ * No counterpart in the reference, whose cache is one contiguous
+ * [B, Hkv, S, D] tensor (ezops/ops/attn_decode.py:60-61); it extends
+ * AttnDecodeOp (ezops/ops/attn_decode.py:9-67) to vLLM-style page pools. */
+int ezops_paged_attn_decode_bf16(const void* Q, const void* K_pages, const void* V_pages, void* Out,
+                                 const int32_t* block_table, const int32_t* kv_lens, int64_t B,
+                                 int64_t H, int64_t Hkv, int64_t D, int64_t num_pages,
+                                 int64_t page_size, int64_t max_pages, int64_t max_kv_len,
+                                 float scale, void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream);
+
 /* Qwen3 per-head QK RMSNorm + half-split RoPE + KV-cache write, one decode step.
  * q [B, H, D] (batch stride q_bstride elements), k/v [B, Hkv, D] (strides
  * k_bstride / v_bstride), q_norm_w / k_norm_w [D] (NULL = unit), cos/sin

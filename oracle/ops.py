@@ -19,6 +19,9 @@ How each function is pinned (tests/test_oracle.py):
   attn_decode      torch SDPA (MATH backend, enable_gqa); S=1 returns V;
                    output inside [min V, max V]; G=1 equals MHA; kv_lens
                    equals truncating the cache
+  paged_attn_decode  gather map: scatter/gather identity over a random page
+                   permutation, one-page reshape, shared pages; equals
+                   attn_decode bit-for-bit on the scattered cache
   qk_norm_rope     pure-Python loops; position 0 is identity; RoPE keeps
                    each (i, i+D/2) pair's norm; cache slot isolation
   o_proj_ffn       pure-Python loops (committed golden vectors)
@@ -32,7 +35,7 @@ import numpy as np
 
 __all__ = [
     "bf16", "gemv", "linear_bf16", "rmsnorm_f32", "rmsnorm_bf16", "softmax", "reduce_sum",
-    "attn_decode", "rope_tables", "qk_norm_rope", "o_proj_ffn", "qwen3_layer",
+    "attn_decode", "paged_to_contiguous", "paged_attn_decode", "rope_tables", "qk_norm_rope", "o_proj_ffn", "qwen3_layer",
 ]
 
 
@@ -119,6 +122,26 @@ def attn_decode(Q, K, V, kv_lens=None, scale=None) -> np.ndarray:
     p = (p / p.sum(axis=-1, keepdims=True)).astype(np.float32)
     o = np.matmul(p, V)  # [B,Hkv,G,D]
     return bf16(o.reshape(B, H, D))
+
+
+def paged_to_contiguous(pages, block_table, page_size):
+    """Gather a page pool [P, Hkv, page_size, D] through block_table [B, M] into
+    the contiguous cache [B, Hkv, M*page_size, D] (row t of sequence b is row
+    t % page_size of pool page block_table[b, t // page_size]).  The
+    reference has no paged cache (ezops/ops/attn_decode.py:60-61 takes one
+    contiguous [B, Hkv, S, D] tensor); this is the layout map alone."""
+    pages = np.asarray(pages)
+    bt = np.asarray(block_table)
+    g = pages[bt]  # [B, M, Hkv, page_size, D]
+    B, M, Hkv, P, D = g.shape
+    return np.ascontiguousarray(g.transpose(0, 2, 1, 3, 4).reshape(B, Hkv, M * P, D))
+
+
+def paged_attn_decode(Q, K_pages, V_pages, block_table, kv_lens, page_size, scale=None) -> np.ndarray:
+    """GQA decode SDPA over a paged cache: ``attn_decode`` on the gathered cache."""
+    K = paged_to_contiguous(K_pages, block_table, page_size)
+    V = paged_to_contiguous(V_pages, block_table, page_size)
+    return attn_decode(Q, K, V, kv_lens, scale)
 
 
 def rope_tables(max_seq_len, head_dim, theta=1e6):

@@ -5,13 +5,13 @@ import pytest
 import torch
 
 import oracle
-from ezops import (AttnDecodeOp, FusedOProjFfnOp, FusedQkNormRopeOp, GemvOp, Qwen3DenseDecodeOp, ReduceOp,
-                   RmsNormOp, SoftmaxOp, get_kernel, list_backends, list_ops, register_kernel)
+from ezops import (AttnDecodeOp, FusedOProjFfnOp, FusedQkNormRopeOp, GemvOp, PagedAttnDecodeOp, Qwen3DenseDecodeOp,
+                   ReduceOp, RmsNormOp, SoftmaxOp, get_kernel, list_backends, list_ops, register_kernel)
 from ezops.ops.utils.accuracy import bitwise_equal, sqnr_db
 from ezops.ops.utils.roofline import RooflineResult, measure_roofline
 
-OPS = ["attn_decode", "fused_o_proj_ffn", "fused_qk_norm_rope", "gemv", "qwen3_dense_decode", "reduce",
-       "rmsnorm", "softmax"]
+OPS = ["attn_decode", "fused_o_proj_ffn", "fused_qk_norm_rope", "gemv", "paged_attn_decode", "qwen3_dense_decode",
+       "reduce", "rmsnorm", "softmax"]
 
 
 def n(x):
@@ -111,6 +111,13 @@ def test_ref_attn_and_qk_rope():
     out = op(Q, K, V, lens)
     ref = oracle.attn_decode(n(Q)[:, :, 0], n(K), n(V), lens.numpy())
     np.testing.assert_allclose(n(out)[:, :, 0], ref, rtol=1e-2, atol=1e-2)
+    pop = PagedAttnDecodeOp(3, 8, 2, 64, page_size=32, max_pages=3, num_pages=11)
+    Q, Kp, Vp, bt, lens = pop.gen_data("cpu")
+    out = pop(Q, Kp, Vp, bt, lens)
+    ref = oracle.paged_attn_decode(n(Q)[:, :, 0], n(Kp), n(Vp), bt.numpy(), lens.numpy(), 32)
+    np.testing.assert_allclose(n(out)[:, :, 0], ref, rtol=1e-2, atol=1e-2)
+    with pytest.raises(ValueError, match="power of two"):
+        PagedAttnDecodeOp(1, 8, 2, 64, page_size=48, max_pages=2)
     op = FusedQkNormRopeOp(2, 8, 64, 50, position=[3, 49], num_kv_heads=2)
     data = op.gen_data("cpu")
     npy = [n(x) for x in data]

@@ -117,6 +117,38 @@ def test_attn_invariants():
     np.testing.assert_allclose(oracle.attn_decode(Q, K, V), mha, rtol=1e-6)
 
 
+def test_paged_gather_pins():
+    """Paged layout map: scattering a contiguous cache into a permuted pool and
+    gathering it back is the identity; one page per sequence with the identity
+    table is a reshape; shared (prefix) pages repeat rows; paged attention on
+    any permutation equals contiguous attention bit-for-bit."""
+    rng = np.random.default_rng(7)
+    B, Hkv, M, P, D = 3, 2, 4, 32, 8
+    K = rng.standard_normal((B, Hkv, M * P, D)).astype(np.float32)
+    perm = rng.permutation(B * M + 5)[: B * M]
+    bt = perm.reshape(B, M)
+    pool = rng.standard_normal((B * M + 5, Hkv, P, D)).astype(np.float32)
+    for b in range(B):
+        for j in range(M):
+            pool[bt[b, j]] = K[b, :, j * P:(j + 1) * P]
+    np.testing.assert_array_equal(oracle.paged_to_contiguous(pool, bt, P), K)
+    one = K.reshape(B, Hkv, 1, M * P, D).transpose(0, 2, 1, 3, 4)[:, 0]
+    np.testing.assert_array_equal(oracle.paged_to_contiguous(one, np.arange(B)[:, None], M * P), K)
+    shared = np.zeros((B, M), dtype=np.int64) + bt[0, 0]
+    g = oracle.paged_to_contiguous(pool, shared, P)
+    np.testing.assert_array_equal(g[:, :, P:2 * P], g[:, :, :P])
+    H = 4
+    Q = rng.standard_normal((B, H, D)).astype(np.float32)
+    V = rng.standard_normal(K.shape).astype(np.float32)
+    vpool = np.zeros_like(pool)
+    for b in range(B):
+        for j in range(M):
+            vpool[bt[b, j]] = V[b, :, j * P:(j + 1) * P]
+    lens = np.array([1, 70, M * P])
+    np.testing.assert_array_equal(oracle.paged_attn_decode(Q, pool, vpool, bt, lens, P),
+                                  oracle.attn_decode(Q, K, V, lens))
+
+
 def test_rope_tables_vs_torch():
     cos, sin = oracle.rope_tables(64, 32, 1e6)
     inv = 1.0 / (1e6 ** (torch.arange(0, 32, 2, dtype=torch.float32) / 32))
