@@ -341,7 +341,29 @@ def main() -> int:
     ms = statistics.mean(step_ms)
     us = ms * 1e3
     gbps = nbytes / (ms * 1e-3) / 1e9
-    del stack
+
+    # The same stack over a paged KV cache (64-row pages dealt in random pool
+    # order, block table read by the attention kernel).
+    from ezops import Qwen3DenseDecodeOp
+
+    PAGE = 64
+    pop = Qwen3DenseDecodeOp(B, SEQ_MAX, backend="hip", kv_lens=lens, norm_weights=True, rope_theta=1e6,
+                             page_size=PAGE, **QWEN3_8B)
+    npg = B * SEQ_MAX // PAGE
+    pstack = []
+    for d in stack:
+        pools = [torch.randn(npg, 8, PAGE, 128, device="cuda").to(torch.bfloat16) for _ in range(2)]
+        bt = torch.randperm(npg, device="cuda").to(torch.int32).reshape(B, SEQ_MAX // PAGE)
+        pstack.append((d[0], *pools, *d[3:], bt))
+
+    def paged_stack():
+        h = data[0]
+        for d in pstack:
+            h = pop(h, *d[1:])
+
+    paged_ms = statistics.mean(time_graph(paged_stack, args.steps, args.warmup, flush_cache)) / STACK
+    log(f"layer {us:.1f} us, paged-cache layer {paged_ms * 1e3:.1f} us")
+    del stack, pstack
     single_ms = statistics.mean(time_graph(lambda: op(*data), args.steps, args.warmup, flush_cache))
     torch.cuda.empty_cache()
 
@@ -389,6 +411,8 @@ def main() -> int:
                   "1 GiB read flush between replays; ms_per_step = replay time / "
                   f"{STACK}; steps = timed replays",
         "us_per_layer_one_layer_graph": round(single_ms * 1e3, 2),
+        "us_per_layer_paged_kv": round(paged_ms * 1e3, 2),
+        "paged_kv": f"same stack over a paged cache: {PAGE}-row pages in random pool order, int32 block table",
         "achieved_GBps": round(gbps, 1),
         "hbm_peak_measured_GBps": round(peak, 1),
         "hbm_probe_GBps": {k: round(v, 1) for k, v in peaks.items()},

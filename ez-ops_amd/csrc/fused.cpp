@@ -109,8 +109,11 @@ extern "C" size_t ezops_qwen3_layer_workspace_size(const ezops_qwen3_layer* p) {
   return multi_kernel_ws(p);
 }
 
-extern "C" int ezops_qwen3_dense_decode_bf16(const ezops_qwen3_layer* p, void* ws, size_t ws_bytes,
-                                             hipStream_t s) {
+namespace {
+// One layer step; block_table != NULL selects the paged cache (K_cache /
+// V_cache are page pools, S = max_pages * page_size).
+int run_layer(const ezops_qwen3_layer* p, const int32_t* block_table, int64_t num_pages, int64_t page_size,
+              void* ws, size_t ws_bytes, hipStream_t s) {
   EZ_REQUIRE(p, "qwen3_dense_decode: null parameter block");
   EZ_REQUIRE(p->hidden && p->K_cache && p->V_cache && p->Wqkv && p->Wo && p->Wgu && p->Wd && p->out && ws,
              "qwen3_dense_decode: null pointer");
@@ -147,6 +150,12 @@ extern "C" int ezops_qwen3_dense_decode_bf16(const ezops_qwen3_layer* p, void* w
   a.B = p->B; a.H = p->H; a.Hkv = p->Hkv; a.S = p->S; a.D = p->D;
   a.kv_lens = p->kv_lens;
   a.Lh = p->max_kv_len;
+  if (block_table) {
+    a.block_table = block_table;
+    a.page_size = int(page_size);
+    a.bt_stride = p->S / page_size;
+    a.num_pages = num_pages;
+  }
   a.scale = 0.f;
   a.qkv = qkv; a.qkv_bs = QKV;
   a.qw = static_cast<const uint16_t*>(p->q_norm_w);
@@ -161,4 +170,20 @@ extern "C" int ezops_qwen3_dense_decode_bf16(const ezops_qwen3_layer* p, void* w
   return run_ffn(att, att_packed, hidden, static_cast<const uint16_t*>(p->Wo), static_cast<const uint16_t*>(p->post_norm_w),
                  Wgu, Wgu + p->IS * p->HS, static_cast<const uint16_t*>(p->Wd), static_cast<uint16_t*>(p->out),
                  p->B, p->HS, p->IS, QR, p->eps, ffn, s);
+}
+}  // namespace
+
+extern "C" int ezops_qwen3_dense_decode_bf16(const ezops_qwen3_layer* p, void* ws, size_t ws_bytes,
+                                             hipStream_t s) {
+  return run_layer(p, nullptr, 0, 0, ws, ws_bytes, s);
+}
+
+extern "C" int ezops_qwen3_dense_decode_paged_bf16(const ezops_qwen3_layer* p, const int32_t* block_table,
+                                                   int64_t num_pages, int64_t page_size, void* ws, size_t ws_bytes,
+                                                   hipStream_t s) {
+  EZ_REQUIRE(p && block_table && p->kv_lens, "qwen3_dense_decode_paged: null pointer (block_table and kv_lens are required)");
+  EZ_REQUIRE(page_size >= 32 && (page_size & (page_size - 1)) == 0 && p->S % page_size == 0,
+             "qwen3_dense_decode_paged: page_size must be a power of two >= 32 dividing S");
+  EZ_REQUIRE(num_pages >= 1 && num_pages <= (int64_t(1) << 31), "qwen3_dense_decode_paged: bad num_pages");
+  return run_layer(p, block_table, num_pages, page_size, ws, ws_bytes, s);
 }

@@ -16,7 +16,7 @@ RMS_EPS = 1e-6
 class Qwen3DenseDecodeHipKernel(BaseKernel):
     def __init__(self, batch: int, seq_len: int, hidden_size: int, intermediate_size: int, num_heads: int,
                  head_dim: int, num_kv_heads: int | None = None, kv_lens=None, norm_weights: bool = False,
-                 rope_theta: float | None = None):
+                 rope_theta: float | None = None, page_size: int | None = None, num_pages: int | None = None):
         num_kv_heads = num_heads if num_kv_heads is None else num_kv_heads
         if num_heads % num_kv_heads:
             raise ValueError(f"num_heads ({num_heads}) must be divisible by num_kv_heads ({num_kv_heads})")
@@ -30,6 +30,13 @@ class Qwen3DenseDecodeHipKernel(BaseKernel):
         self.kv_lens = None if kv_lens is None else [int(x) for x in kv_lens]
         self.norm_weights = norm_weights
         self.rope = rope_theta is not None
+        if page_size is not None:
+            if page_size < 32 or page_size & (page_size - 1) or seq_len % page_size:
+                raise ValueError(f"page_size ({page_size}) must be a power of two >= 32 dividing seq_len ({seq_len})")
+            if self.kv_lens is None:
+                raise ValueError("a paged cache requires kv_lens")
+            num_pages = batch * (seq_len // page_size) if num_pages is None else num_pages
+        self.page_size, self.num_pages = page_size, num_pages
         self._ws = _hip.Workspace()
         self._lens_dev: dict = {}
 
@@ -43,17 +50,29 @@ class Qwen3DenseDecodeHipKernel(BaseKernel):
         return t
 
     def __call__(self, hidden, K_cache, V_cache, Wqkv, Wo, Wgu, Wd, *extra):
+        """Paged cache: K_cache / V_cache are page pools and the block table
+        is the last input."""
+        bt = None
+        if self.page_size is not None:
+            if not extra:
+                raise ValueError("paged cache: the block table is the last input")
+            *extra, bt = extra
         want = (4 if self.norm_weights else 0) + (2 if self.rope else 0)
         if len(extra) != want:
             raise ValueError(f"expected {want} extra inputs (norm weights / rope tables), got {len(extra)}")
         nw = list(extra[:4]) if self.norm_weights else [None] * 4
         cos, sin = extra[-2:] if self.rope else (None, None)
-        dev = _hip.require_gpu(hidden, K_cache, V_cache, Wqkv, Wo, Wgu, Wd, *extra)
+        dev = _hip.require_gpu(hidden, K_cache, V_cache, Wqkv, Wo, Wgu, Wd, *extra, *([] if bt is None else [bt]))
         bf = torch.bfloat16
         B, S, HS, IS, H, D, Hkv = self.B, self.S, self.HS, self.IS, self.H, self.D, self.Hkv
         _hip.check(hidden, "hidden", (B, HS), bf)
-        _hip.check(K_cache, "K_cache", (B, Hkv, S, D), bf)
-        _hip.check(V_cache, "V_cache", (B, Hkv, S, D), bf)
+        if bt is None:
+            kv_shape = (B, Hkv, S, D)
+        else:
+            kv_shape = (self.num_pages, Hkv, self.page_size, D)
+            _hip.check(bt, "block_table", (B, S // self.page_size), torch.int32)
+        _hip.check(K_cache, "K_cache", kv_shape, bf)
+        _hip.check(V_cache, "V_cache", kv_shape, bf)
         _hip.check(Wqkv, "Wqkv", ((H + 2 * Hkv) * D, HS), bf)
         _hip.check(Wo, "Wo", (HS, H * D), bf)
         _hip.check(Wgu, "Wgu", (2 * IS, HS), bf)
@@ -77,5 +96,9 @@ class Qwen3DenseDecodeHipKernel(BaseKernel):
         )
         pp = ctypes.byref(p)
         ws = self._ws.get(_hip.size("ezops_qwen3_layer_workspace_size", pp), dev)
-        _hip.call("ezops_qwen3_dense_decode_bf16", pp, ws.data_ptr(), ws.numel(), _hip.stream(dev))
+        if bt is None:
+            _hip.call("ezops_qwen3_dense_decode_bf16", pp, ws.data_ptr(), ws.numel(), _hip.stream(dev))
+        else:
+            _hip.call("ezops_qwen3_dense_decode_paged_bf16", pp, bt.data_ptr(), self.num_pages, self.page_size,
+                      ws.data_ptr(), ws.numel(), _hip.stream(dev))
         return out

@@ -23,6 +23,12 @@ Qwen3 mode (keyword-only ctor options, for the Qwen3-8B benchmark config):
     (``forward(..., cos, sin)``); q/k norm + RoPE then follow the fused
     QK-norm+RoPE stage exactly (fp32 pipeline, one bf16 rounding,
     ezops/ops/fused_qk_norm_rope.py:138-169).
+  * ``page_size`` (extension, no reference counterpart): the cache is paged.
+    ``K_cache`` / ``V_cache`` are page pools ``[num_pages, Hkv, page_size, D]``
+    (``num_pages`` default ``batch * seq_len / page_size``) and ``forward``
+    takes the int32 block table ``[batch, seq_len / page_size]`` as its last
+    input; logical page ``j`` of sequence ``b`` is pool page
+    ``block_table[b, j]``.  Requires ``kv_lens``.
 """
 
 from collections.abc import Sequence
@@ -57,7 +63,8 @@ class Qwen3DenseDecodeOp(Op):
     def __init__(self, batch: int, seq_len: int, hidden_size: int, intermediate_size: int,
                  num_heads: int, head_dim: int, backend: str = "ref",
                  num_kv_heads: int | None = None, *, kv_lens=None,
-                 norm_weights: bool = False, rope_theta: float | None = None):
+                 norm_weights: bool = False, rope_theta: float | None = None,
+                 page_size: int | None = None, num_pages: int | None = None):
         if seq_len < 1:
             raise ValueError(f"seq_len ({seq_len}) must be >= 1")
         self.batch = batch
@@ -81,6 +88,15 @@ class Qwen3DenseDecodeOp(Op):
                 if not 1 <= n <= seq_len:
                     raise ValueError(f"kv_lens entry {n} must be in [1, {seq_len}]")
         self.kv_lens = kv_lens
+        if page_size is not None:
+            if page_size < 32 or page_size & (page_size - 1) or seq_len % page_size:
+                raise ValueError(f"page_size ({page_size}) must be a power of two >= 32 dividing seq_len ({seq_len})")
+            if kv_lens is None:
+                raise ValueError("a paged cache requires kv_lens")
+            num_pages = batch * (seq_len // page_size) if num_pages is None else num_pages
+            if num_pages < 1:
+                raise ValueError("num_pages must be >= 1")
+        self.page_size, self.num_pages = page_size, num_pages
         self.norm_weights = norm_weights
         self.rope_theta = rope_theta
         self.q_rows = num_heads * head_dim
@@ -90,7 +106,8 @@ class Qwen3DenseDecodeOp(Op):
             cls = get_kernel("qwen3_dense_decode", backend)
             self._kernel = cls(batch, seq_len, hidden_size, intermediate_size, num_heads, head_dim,
                                num_kv_heads=self.num_kv_heads, kv_lens=kv_lens,
-                               norm_weights=norm_weights, rope_theta=rope_theta)
+                               norm_weights=norm_weights, rope_theta=rope_theta,
+                               **({} if page_size is None else {"page_size": page_size, "num_pages": num_pages}))
         else:
             self._kernel = self._ref_forward
 
@@ -105,8 +122,12 @@ class Qwen3DenseDecodeOp(Op):
         bf = dict(dtype=torch.bfloat16, device=dev)
         H, I = self.hidden_size, self.intermediate_size
         hidden = randn(self.batch, H, **bf)
-        K_cache = randn(self.batch, self.num_kv_heads, self.seq_len, self.head_dim, **bf)
-        V_cache = randn(self.batch, self.num_kv_heads, self.seq_len, self.head_dim, **bf)
+        if self.page_size is None:
+            kv_shape = (self.batch, self.num_kv_heads, self.seq_len, self.head_dim)
+        else:
+            kv_shape = (self.num_pages, self.num_kv_heads, self.page_size, self.head_dim)
+        K_cache = randn(*kv_shape, **bf)
+        V_cache = randn(*kv_shape, **bf)
         Wqkv = randn(self.q_rows + 2 * self.kv_rows, H, **bf, scale=H ** -0.5)
         Wo = randn(H, self.q_rows, **bf, scale=self.q_rows ** -0.5)
         Wgu = randn(2 * I, H, **bf, scale=H ** -0.5)
@@ -120,6 +141,11 @@ class Qwen3DenseDecodeOp(Op):
                 data += [torch.empty(self.seq_len, self.head_dim, **bf)] * 2
             else:
                 data += list(rope_tables(self.seq_len, self.head_dim, self.rope_theta, dev))
+        if self.page_size is not None:
+            M = self.seq_len // self.page_size
+            n = self.batch * M
+            ids = torch.randperm(self.num_pages)[:n] if self.num_pages >= n else torch.randint(0, self.num_pages, (n,))
+            data.append(ids.reshape(self.batch, M).to(torch.int32).to(dev))
         return tuple(data)
 
     def _split_extra(self, extra):
@@ -132,6 +158,23 @@ class Qwen3DenseDecodeOp(Op):
         return nw, rope
 
     def _ref_forward(self, hidden, K_cache, V_cache, Wqkv, Wo, Wgu, Wd, *extra):
+        if self.page_size is not None:
+            # gather the sequences' pages, run the contiguous step, and write
+            # the decoded token's rows back to their pool pages
+            from .paged_attn_decode import paged_to_contiguous
+
+            *extra, bt = extra
+            Kc, Vc = paged_to_contiguous(K_cache, bt).clone(), paged_to_contiguous(V_cache, bt).clone()
+            out = self._ref_contiguous(hidden, Kc, Vc, Wqkv, Wo, Wgu, Wd, *extra)
+            pos = torch.tensor(self.lens(), dtype=torch.long, device=hidden.device) - 1
+            b = torch.arange(hidden.shape[0], device=hidden.device)
+            page = bt.long()[b, pos // self.page_size]
+            K_cache[page, :, pos % self.page_size] = Kc[b, :, pos]
+            V_cache[page, :, pos % self.page_size] = Vc[b, :, pos]
+            return out
+        return self._ref_contiguous(hidden, K_cache, V_cache, Wqkv, Wo, Wgu, Wd, *extra)
+
+    def _ref_contiguous(self, hidden, K_cache, V_cache, Wqkv, Wo, Wgu, Wd, *extra):
         (in_w, q_w, k_w, post_w), rope = self._split_extra(extra)
         B, D = hidden.shape[0], self.head_dim
         dev = hidden.device

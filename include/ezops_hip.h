@@ -194,6 +194,19 @@ size_t ezops_qwen3_layer_workspace_size(const ezops_qwen3_layer* p);
 int ezops_qwen3_dense_decode_bf16(const ezops_qwen3_layer* p, void* workspace,
                                   size_t workspace_bytes, hipStream_t stream);
 
+/* The same layer step over a paged KV cache: K_cache / V_cache are page pools
+ * [num_pages, Hkv, page_size, D]; block_table [B, S / page_size] int32 maps
+ * logical page j of sequence b to a pool page (layout and clamping as in
+ * ezops_paged_attn_decode_bf16).  kv_lens is required; the decoded token's
+ * k/v go to row kv_lens[b]-1 of the sequence (pool page
+ * block_table[b][(kv_lens[b]-1) / page_size]).  page_size: power of two >= 32
+ * dividing S.  Workspace: ezops_qwen3_layer_workspace_size(p).
+ * No counterpart in the reference (its cache is contiguous,
+ * ezops/ops/qwen3_dense_decode.py:142-176); extends Qwen3DenseDecodeOp. */
+int ezops_qwen3_dense_decode_paged_bf16(const ezops_qwen3_layer* p, const int32_t* block_table,
+                                        int64_t num_pages, int64_t page_size, void* workspace,
+                                        size_t workspace_bytes, hipStream_t stream);
+
 /* STREAM-style HBM probes used to measure the chip's bandwidth peak
  * (replaces benchmarks/hardware/memory/hbm_saturation.cu:49-90):
  * kind 0 = read (sum into out[0..]; allocates in the caches, used as the

@@ -145,3 +145,30 @@ def test_ref_fused_and_layer():
     assert op.check(out, torch.from_numpy(ref))
     np.testing.assert_allclose(n(data[1]), Kc, rtol=1e-2, atol=1e-2)
     np.testing.assert_array_equal(n(data[2]), Vc)
+
+
+def test_ref_layer_paged_cache():
+    """Paged reference layer = oracle layer on the gathered cache; only the
+    decoded token's rows change in the pools."""
+    torch.manual_seed(3)
+    op = Qwen3DenseDecodeOp(2, 64, 128, 192, 4, 32, num_kv_heads=2, kv_lens=[64, 33], norm_weights=True,
+                            rope_theta=1e6, page_size=32, num_pages=7)
+    data = op.gen_data("cpu")
+    bt = data[-1]
+    V0 = data[2].clone()
+    npy = [n(x) for x in data[:-1]]
+    Kc0 = oracle.paged_to_contiguous(npy[1], bt.numpy(), 32)
+    Vc0 = oracle.paged_to_contiguous(npy[2], bt.numpy(), 32)
+    out = op(*data)
+    ref, Kc, Vc = oracle.qwen3_layer(npy[0], Kc0, Vc0, *npy[3:7], 4, 2, 32, kv_lens=[64, 33], in_norm_w=npy[7],
+                                     q_norm_w=npy[8], k_norm_w=npy[9], post_norm_w=npy[10], cos=npy[11],
+                                     sin=npy[12])
+    assert op.check(out, torch.from_numpy(ref))
+    np.testing.assert_allclose(oracle.paged_to_contiguous(n(data[1]), bt.numpy(), 32), Kc, rtol=1e-2, atol=1e-2)
+    np.testing.assert_array_equal(oracle.paged_to_contiguous(n(data[2]), bt.numpy(), 32), Vc)
+    changed = (data[2] != V0).any(dim=(1, 3)).nonzero().tolist()  # (page, row) pairs
+    assert sorted(changed) == sorted([[int(bt[0, 1]), 31], [int(bt[1, 1]), 0]])
+    with pytest.raises(ValueError, match="kv_lens"):
+        Qwen3DenseDecodeOp(1, 64, 128, 192, 4, 32, page_size=32)
+    with pytest.raises(ValueError, match="dividing"):
+        Qwen3DenseDecodeOp(1, 80, 128, 192, 4, 32, kv_lens=[3], page_size=32)

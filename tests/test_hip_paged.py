@@ -11,7 +11,7 @@ import pytest
 import torch
 
 import oracle
-from ezops import AttnDecodeOp, PagedAttnDecodeOp
+from ezops import AttnDecodeOp, PagedAttnDecodeOp, Qwen3DenseDecodeOp
 from ezops.ops.paged_attn_decode import paged_to_contiguous
 
 pytestmark = pytest.mark.gpu
@@ -86,3 +86,35 @@ def test_paged_graph_replays():
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
         op(Q, Kp, Vp, bt, lens)  # eager work between replays
+
+
+QWEN3_8B = dict(hidden_size=4096, intermediate_size=12288, num_heads=32, head_dim=128)
+
+
+@pytest.mark.parametrize("batch,seq_len,page_size", [(1, 16384, 64), (4, 4096, 32), (16, 4096, 256)])
+def test_paged_layer_equals_contiguous(batch, seq_len, page_size):
+    """The Qwen3-8B layer over a paged cache: output bit-identical to the
+    contiguous layer on the gathered cache, the decoded rows land in the
+    right pool pages and nothing else in the pools changes."""
+    torch.manual_seed(batch)
+    rng = np.random.default_rng(batch)
+    lens = rng.integers(min(1024, seq_len), seq_len + 1, size=batch).tolist()
+    mode = dict(kv_lens=lens, norm_weights=True, rope_theta=1e6)
+    pop = Qwen3DenseDecodeOp(batch, seq_len, backend="hip", num_kv_heads=8, page_size=page_size,
+                             num_pages=batch * seq_len // page_size + 3, **QWEN3_8B, **mode)
+    data = list(pop.gen_data())
+    bt = data[-1]
+    Kc = paged_to_contiguous(data[1], bt).contiguous()
+    Vc = paged_to_contiguous(data[2], bt).contiguous()
+    K0, V0 = data[1].clone(), data[2].clone()
+    out = pop(*data)
+    cop = Qwen3DenseDecodeOp(batch, seq_len, backend="hip", num_kv_heads=8, **QWEN3_8B, **mode)
+    cout = cop(data[0], Kc, Vc, *data[3:-1])
+    assert torch.equal(out, cout)
+    assert torch.equal(paged_to_contiguous(data[1], bt), Kc)
+    assert torch.equal(paged_to_contiguous(data[2], bt), Vc)
+    touched = torch.zeros(K0.shape[0], page_size, dtype=torch.bool, device=DEV)
+    for b, L in enumerate(lens):
+        touched[int(bt[b, (L - 1) // page_size]), (L - 1) % page_size] = True
+    rows = lambda t: t.transpose(1, 2)[~touched]  # noqa: E731  (page, row) pairs not written
+    assert torch.equal(rows(data[1]), rows(K0)) and torch.equal(rows(data[2]), rows(V0))
