@@ -117,6 +117,31 @@ def layer_bytes(batch: int, lens) -> int:
     return weights + kv + act
 
 
+def decode_step(torch, data, lens, batch: int, steps: int, warmup: int, flush) -> dict:
+    """A whole Qwen3-8B decode step: 36 layers (distinct weight and cache
+    copies) + final RMSNorm + the 151,936-row LM head, one graph replay per
+    step, caches flushed between replays."""
+    from ezops import Qwen3DecodeStepOp
+
+    NL, VOCAB = 36, 151936
+    op = Qwen3DecodeStepOp(batch, SEQ_MAX, num_layers=NL, backend="hip", vocab_size=VOCAB, kv_lens=lens,
+                           norm_weights=True, rope_theta=1e6, **QWEN3_8B)
+    layers = [tuple(t.clone() for t in data[1:11]) for _ in range(NL)]
+    g = torch.Generator(device="cuda").manual_seed(11)
+    lm = (torch.randn(VOCAB, 4096, generator=g, device="cuda") * 4096 ** -0.5).to(torch.bfloat16)
+    fw = (1 + 0.1 * torch.randn(4096, generator=g, device="cuda")).to(torch.bfloat16)
+    args = (data[0], layers, data[11], data[12], fw, lm)
+    ms = statistics.mean(time_graph(lambda: op(*args), steps, warmup, flush))
+    nbytes = NL * layer_bytes(batch, lens) + VOCAB * 4096 * 2 + batch * VOCAB * 2
+    del layers, lm
+    torch.cuda.empty_cache()
+    return {"layers": NL, "vocab": VOCAB, "ms_per_step": round(ms, 4), "tokens_per_s": round(batch / ms * 1e3, 1),
+            "us_per_layer_amortised": round(ms * 1e3 / NL, 2), "algorithmic_bytes": nbytes,
+            "achieved_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "timing": "HIP events around each graph replay of the whole step (36 layers + LM head), "
+                      "1 GiB read flush between replays"}
+
+
 def cpu_baseline(torch, op, data, lens, budget_s: float = 20.0) -> dict:
     """The numpy oracle (fp32 BLAS restatement of the reference layer) on this host."""
     import numpy as np
@@ -283,6 +308,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-ops", action="store_true", help="skip the per-op table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-step", action="store_true", help="skip the 36-layer decode-step timing")
     ap.add_argument("--batch", type=int, default=1, help="layer batch (headline is 1)")
     ap.add_argument("--profile-kernel", choices=["gate_up", "copy", "layer"],
                     help="only launch this kernel 10x between read flushes (for rocprofv3 counter runs)")
@@ -437,6 +463,11 @@ def main() -> int:
                                "3 rotating weight copies"},
     }
 
+    if not args.no_step:
+        log("timing the 36-layer decode step + LM head")
+        result["decode_step"] = decode_step(torch, data, lens, B, max(5, args.steps // 3), 2, flush_cache)
+        log(f"decode step {result['decode_step']['ms_per_step']:.3f} ms, "
+            f"{result['decode_step']['tokens_per_s']:.0f} tokens/s")
     if not args.no_cpu:
         log("CPU baseline: numpy oracle of the same layer step")
         cb = cpu_baseline(torch, op, data, lens)

@@ -11,6 +11,8 @@
 //                  out = o_proj + FFN(attn, hidden)
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 
 #include "internal.h"
 #include "status.h"
@@ -186,4 +188,68 @@ extern "C" int ezops_qwen3_dense_decode_paged_bf16(const ezops_qwen3_layer* p, c
              "qwen3_dense_decode_paged: page_size must be a power of two >= 32 dividing S");
   EZ_REQUIRE(num_pages >= 1 && num_pages <= (int64_t(1) << 31), "qwen3_dense_decode_paged: bad num_pages");
   return run_layer(p, block_table, num_pages, page_size, ws, ws_bytes, s);
+}
+
+// ---------------------------------------------------------------------------
+// Multi-layer decode step: n_layers layer steps chained on one stream, the
+// hidden state ping-ponging through the workspace, then the optional final
+// RMSNorm + LM head.  Every launch is stream-ordered and allocation-free, so
+// a caller captures the whole step in one HIP graph.
+namespace {
+bool same_shape(const ezops_qwen3_layer& a, const ezops_qwen3_layer& b) {
+  return a.B == b.B && a.S == b.S && a.HS == b.HS && a.IS == b.IS && a.H == b.H && a.Hkv == b.Hkv && a.D == b.D;
+}
+size_t step_ws(const ezops_qwen3_layer* l0, int64_t vocab) {
+  const size_t hid = align256(size_t(l0->B * l0->HS) * 2);
+  const size_t head = vocab > 0 ? align256(ezops_linear_stage_workspace_size(l0->B, l0->HS, 1)) : 0;
+  return 2 * hid + std::max(align256(multi_kernel_ws(l0)), head);
+}
+}  // namespace
+
+extern "C" size_t ezops_qwen3_decode_step_workspace_size(const ezops_qwen3_layer* layers, int64_t n_layers,
+                                                         int64_t vocab) {
+  if (!layers || n_layers < 1 || !ezops_qwen3_layer_workspace_size(layers)) return 0;
+  return step_ws(layers, vocab);
+}
+
+extern "C" int ezops_qwen3_decode_step_bf16(const ezops_qwen3_layer* layers, int64_t n_layers,
+                                            const int32_t* block_table, int64_t num_pages, int64_t page_size,
+                                            const void* final_norm_w, const void* lm_head, int64_t vocab,
+                                            void* logits, void* ws, size_t ws_bytes, hipStream_t s) {
+  EZ_REQUIRE(layers && n_layers >= 1 && ws, "qwen3_decode_step: null pointer or no layers");
+  const ezops_qwen3_layer& l0 = layers[0];
+  EZ_REQUIRE(l0.hidden && layers[n_layers - 1].out, "qwen3_decode_step: layers[0].hidden and the last out are required");
+  EZ_REQUIRE(vocab >= 0 && (vocab == 0 || (lm_head && logits)), "qwen3_decode_step: lm_head and logits go with vocab > 0");
+  for (int64_t i = 1; i < n_layers; ++i)
+    EZ_REQUIRE(same_shape(l0, layers[i]), "qwen3_decode_step: layer %lld shape differs from layer 0", (long long)i);
+  EZ_REQUIRE(ws_bytes >= ezops_qwen3_decode_step_workspace_size(layers, n_layers, vocab),
+             "qwen3_decode_step: workspace too small");
+  if (block_table) {
+    EZ_REQUIRE(page_size >= 32 && (page_size & (page_size - 1)) == 0 && l0.S % page_size == 0 && num_pages >= 1 &&
+                   num_pages <= (int64_t(1) << 31),
+               "qwen3_decode_step: page_size must be a power of two >= 32 dividing S");
+  }
+  Carve c{static_cast<char*>(ws)};
+  uint16_t* hbuf[2] = {c.take<uint16_t>(size_t(l0.B * l0.HS) * 2), c.take<uint16_t>(size_t(l0.B * l0.HS) * 2)};
+  void* lws = c.p;
+  const size_t lws_bytes = ws_bytes - size_t(c.p - static_cast<char*>(ws));
+  const void* h = l0.hidden;
+  for (int64_t i = 0; i < n_layers; ++i) {
+    ezops_qwen3_layer p = layers[i];
+    p.hidden = h;
+    if (i + 1 < n_layers) p.out = hbuf[i & 1];
+    EZ_REQUIRE(!block_table || p.kv_lens, "qwen3_decode_step: a paged cache requires kv_lens");
+    const int rc = run_layer(&p, block_table, num_pages, page_size, lws, lws_bytes, s);
+    if (rc) return rc;
+    h = p.out;
+  }
+  if (vocab == 0) return 0;
+  LinearArgs l{};
+  l.X = static_cast<const uint16_t*>(h); l.ldx = l0.HS;
+  l.W = static_cast<const uint16_t*>(lm_head);
+  l.Y = static_cast<uint16_t*>(logits); l.ldy = vocab;
+  l.M = l0.B; l.N = vocab; l.K = l0.HS;
+  l.norm = 1; l.norm_w = static_cast<const uint16_t*>(final_norm_w); l.eps = l0.eps;
+  l.epi = kEpiStore; l.xn_ws = static_cast<uint16_t*>(lws);
+  return launch_linear(l, s);
 }

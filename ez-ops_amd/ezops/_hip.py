@@ -59,6 +59,9 @@ SIGNATURES: dict[str, tuple] = {
     "ezops_qwen3_layer_workspace_size": (_sz, [C.POINTER(Qwen3LayerParams)]),
     "ezops_qwen3_dense_decode_bf16": (_i32, [C.POINTER(Qwen3LayerParams), _p, _sz, _p]),
     "ezops_qwen3_dense_decode_paged_bf16": (_i32, [C.POINTER(Qwen3LayerParams), _p, _i64, _i64, _p, _sz, _p]),
+    "ezops_qwen3_decode_step_workspace_size": (_sz, [C.POINTER(Qwen3LayerParams), _i64, _i64]),
+    "ezops_qwen3_decode_step_bf16": (_i32, [C.POINTER(Qwen3LayerParams), _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p,
+                                            _sz, _p]),
     "ezops_hbm_probe": (_i32, [_i32, _p, _p, _p, _i64, _f32, _p]),
     "ezops_mfma_probe": (_i32, [_i32, _p, _i64, _i64, _p]),
 }

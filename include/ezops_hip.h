@@ -207,6 +207,26 @@ int ezops_qwen3_dense_decode_paged_bf16(const ezops_qwen3_layer* p, const int32_
                                         int64_t num_pages, int64_t page_size, void* workspace,
                                         size_t workspace_bytes, hipStream_t stream);
 
+/* A multi-layer decode step: n_layers layer steps (same shapes, each with its
+ * own weights and cache) chained on one stream, then, if vocab > 0, the final
+ * RMSNorm (final_norm_w [HS] or NULL = unit) and the LM head
+ * (lm_head [vocab, HS]) into logits [B, vocab] bf16.
+ * Input: layers[0].hidden.  Output hidden state: layers[n_layers-1].out.  The
+ * other hidden/out fields are ignored (the hidden state moves through the
+ * workspace).  block_table != NULL: every layer's cache is a page pool with
+ * the same block table, page_size and num_pages (as in
+ * ezops_qwen3_dense_decode_paged_bf16).  Allocation-free and stream-ordered:
+ * the whole step can be captured in one HIP graph.
+ * No counterpart in the reference, which stops at one layer
+ * (ezops/ops/qwen3_dense_decode.py:9-176); it is that layer's caller. */
+size_t ezops_qwen3_decode_step_workspace_size(const ezops_qwen3_layer* layers, int64_t n_layers,
+                                              int64_t vocab);
+int ezops_qwen3_decode_step_bf16(const ezops_qwen3_layer* layers, int64_t n_layers,
+                                 const int32_t* block_table, int64_t num_pages, int64_t page_size,
+                                 const void* final_norm_w, const void* lm_head, int64_t vocab,
+                                 void* logits, void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream);
+
 /* STREAM-style HBM probes used to measure the chip's bandwidth peak
  * (replaces benchmarks/hardware/memory/hbm_saturation.cu:49-90):
  * kind 0 = read (sum into out[0..]; allocates in the caches, used as the

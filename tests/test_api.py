@@ -5,12 +5,13 @@ import pytest
 import torch
 
 import oracle
-from ezops import (AttnDecodeOp, FusedOProjFfnOp, FusedQkNormRopeOp, GemvOp, PagedAttnDecodeOp, Qwen3DenseDecodeOp,
+from ezops import (AttnDecodeOp, FusedOProjFfnOp, FusedQkNormRopeOp, GemvOp, PagedAttnDecodeOp, Qwen3DecodeStepOp,
+                   Qwen3DenseDecodeOp,
                    ReduceOp, RmsNormOp, SoftmaxOp, get_kernel, list_backends, list_ops, register_kernel)
 from ezops.ops.utils.accuracy import bitwise_equal, sqnr_db
 from ezops.ops.utils.roofline import RooflineResult, measure_roofline
 
-OPS = ["attn_decode", "fused_o_proj_ffn", "fused_qk_norm_rope", "gemv", "paged_attn_decode", "qwen3_dense_decode",
+OPS = ["attn_decode", "fused_o_proj_ffn", "fused_qk_norm_rope", "gemv", "paged_attn_decode", "qwen3_decode_step", "qwen3_dense_decode",
        "reduce", "rmsnorm", "softmax"]
 
 
@@ -172,3 +173,28 @@ def test_ref_layer_paged_cache():
         Qwen3DenseDecodeOp(1, 64, 128, 192, 4, 32, page_size=32)
     with pytest.raises(ValueError, match="dividing"):
         Qwen3DenseDecodeOp(1, 80, 128, 192, 4, 32, kv_lens=[3], page_size=32)
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_ref_decode_step_vs_oracle_chain(paged):
+    """Multi-layer step = the oracle layer applied layer by layer, then the
+    final RMSNorm and the LM head (bf16 staging of the normed state)."""
+    torch.manual_seed(5)
+    kw = dict(page_size=32, num_pages=9) if paged else {}
+    op = Qwen3DecodeStepOp(2, 64, 128, 192, 4, 32, 3, num_kv_heads=2, vocab_size=50, kv_lens=[64, 40],
+                           norm_weights=True, rope_theta=1e6, **kw)
+    hidden, layers, cos, sin, fw, lm, bt = op.gen_data("cpu")
+    npl = [[n(t) for t in layer] for layer in layers]
+    h_ref = n(hidden)
+    for L in npl:
+        K, V = L[0], L[1]
+        if paged:
+            K, V = oracle.paged_to_contiguous(K, bt.numpy(), 32), oracle.paged_to_contiguous(V, bt.numpy(), 32)
+        h_ref, _, _ = oracle.qwen3_layer(h_ref, K, V, *L[2:6], 4, 2, 32, kv_lens=[64, 40], in_norm_w=L[6],
+                                         q_norm_w=L[7], k_norm_w=L[8], post_norm_w=L[9], cos=n(cos), sin=n(sin))
+    logits_ref = oracle.linear_bf16(oracle.rmsnorm_bf16(h_ref, n(fw)), n(lm))
+    h, logits = op(hidden, layers, cos, sin, fw, lm, bt)
+    assert op.check(h, torch.from_numpy(h_ref))
+    assert op.check(logits, torch.from_numpy(logits_ref))
+    with pytest.raises(ValueError, match="num_layers"):
+        Qwen3DecodeStepOp(1, 64, 128, 192, 4, 32, 0)
