@@ -91,5 +91,20 @@ struct AttnArgs {
 size_t attn_workspace_size(int64_t B, int64_t H, int64_t Hkv, int64_t S, int64_t D);
 int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s);
 
+// Prefill attention: new tokens of sequence b are rows cu[b] .. cu[b+1]-1 of
+// Q / Out (row strides q_rs / o_rs, head h at + h*D) and sit at cache rows
+// past[b] + i; each attends cache rows [0, its row] (causal).
+struct PrefillAttnArgs {
+  const uint16_t* Q; int64_t q_rs;
+  const uint16_t* K; const uint16_t* V;  // [B, Hkv, S, D] or pools [pages, Hkv, page_size, D]
+  uint16_t* Out; int64_t o_rs;
+  const int32_t* cu; const int32_t* past;  // [B + 1], [B] (NULL = 0)
+  const int32_t* block_table; int64_t bt_stride; int page_size; int64_t num_pages;
+  int64_t B, H, Hkv, S, D, max_q;
+  float scale;
+};
+int launch_prefill_attn(const PrefillAttnArgs& a, hipStream_t s);
+int launch_silu_mul(const uint16_t* gu, uint16_t* out, int64_t T, int64_t IS, hipStream_t s);
+
 
 }  // namespace ez

@@ -12,6 +12,7 @@ from .ops.fused_o_proj_ffn import FusedOProjFfnOp
 from .ops.fused_qk_norm_rope import FusedQkNormRopeOp
 from .ops.gemv import GemvOp
 from .ops.paged_attn_decode import PagedAttnDecodeOp
+from .ops.prefill_attn import PrefillAttnOp
 from .ops.qwen3_decode_step import Qwen3DecodeStepOp
 from .ops.qwen3_dense_decode import Qwen3DenseDecodeOp
 from .ops.reduce import ReduceOp
@@ -21,7 +22,7 @@ from .ops.utils.roofline import RooflineResult
 from .registry import get_kernel, list_backends, list_ops, register_kernel
 
 __all__ = [
-    "AttnDecodeOp", "FusedOProjFfnOp", "FusedQkNormRopeOp", "GemvOp", "Op", "PagedAttnDecodeOp", "Qwen3DecodeStepOp", "Qwen3DenseDecodeOp",
+    "AttnDecodeOp", "FusedOProjFfnOp", "FusedQkNormRopeOp", "GemvOp", "Op", "PagedAttnDecodeOp", "PrefillAttnOp", "Qwen3DecodeStepOp", "Qwen3DenseDecodeOp",
     "ReduceOp", "RmsNormOp", "RooflineResult", "SoftmaxOp", "get_kernel", "list_backends", "list_ops",
     "register_kernel",
 ]

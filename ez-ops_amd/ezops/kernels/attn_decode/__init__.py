@@ -1,1 +1,1 @@
-from . import attn_decode_hip, paged_attn_decode_hip  # noqa: F401
+from . import attn_decode_hip, paged_attn_decode_hip, prefill_attn_hip  # noqa: F401

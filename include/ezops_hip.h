@@ -134,6 +134,23 @@ int ezops_paged_attn_decode_bf16(const void* Q, const void* K_pages, const void*
                                  float scale, void* workspace, size_t workspace_bytes,
                                  hipStream_t stream);
 
+/* Prefill attention: causal GQA flash attention for a chunk of new tokens.
+ * Sequence b's new tokens are rows cu_seqlens[b] .. cu_seqlens[b+1]-1 of
+ * Q / Out ([T, H, D] bf16, T = cu_seqlens[B]); they already sit in the cache
+ * at rows past_lens[b] + i (past_lens NULL = 0), and token i attends cache
+ * rows [0, past_lens[b] + i].  Cache K/V [B, Hkv, S, D], or page pools
+ * [num_pages, Hkv, page_size, D] with block_table [B, S / page_size] when
+ * block_table != NULL.  max_q_len: host bound on the per-sequence token
+ * counts (grid size).  D = 128; H / Hkv in {1, 2, 4, 8}; scale <= 0 selects
+ * 1/sqrt(D).  Rows at or beyond S are skipped.
+ * No counterpart in the reference (decode only, ezops/ops/attn_decode.py:9-67):
+ * the step before the decode path, writing the cache it reads. */
+int ezops_prefill_attn_bf16(const void* Q, const void* K, const void* V, void* Out,
+                            const int32_t* cu_seqlens, const int32_t* past_lens, int64_t B, int64_t H,
+                            int64_t Hkv, int64_t S, int64_t D, int64_t max_q_len,
+                            const int32_t* block_table, int64_t num_pages, int64_t page_size,
+                            float scale, hipStream_t stream);
+
 /* Qwen3 per-head QK RMSNorm + half-split RoPE + KV-cache write, one decode step.
  * q [B, H, D] (batch stride q_bstride elements), k/v [B, Hkv, D] (strides
  * k_bstride / v_bstride), q_norm_w / k_norm_w [D] (NULL = unit), cos/sin

@@ -19,6 +19,8 @@ How each function is pinned (tests/test_oracle.py):
   attn_decode      torch SDPA (MATH backend, enable_gqa); S=1 returns V;
                    output inside [min V, max V]; G=1 equals MHA; kv_lens
                    equals truncating the cache
+  prefill_attn     each token equals attn_decode with kv_len = past + i + 1;
+                   torch SDPA is_causal on a fresh prompt
   paged_attn_decode  gather map: scatter/gather identity over a random page
                    permutation, one-page reshape, shared pages; equals
                    attn_decode bit-for-bit on the scattered cache
@@ -35,7 +37,7 @@ import numpy as np
 
 __all__ = [
     "bf16", "gemv", "linear_bf16", "rmsnorm_f32", "rmsnorm_bf16", "softmax", "reduce_sum",
-    "attn_decode", "paged_to_contiguous", "paged_attn_decode", "rope_tables", "qk_norm_rope", "o_proj_ffn", "qwen3_layer",
+    "attn_decode", "paged_to_contiguous", "paged_attn_decode", "prefill_attn", "rope_tables", "qk_norm_rope", "o_proj_ffn", "qwen3_layer",
 ]
 
 
@@ -142,6 +144,35 @@ def paged_attn_decode(Q, K_pages, V_pages, block_table, kv_lens, page_size, scal
     K = paged_to_contiguous(K_pages, block_table, page_size)
     V = paged_to_contiguous(V_pages, block_table, page_size)
     return attn_decode(Q, K, V, kv_lens, scale)
+
+
+def prefill_attn(Q, K, V, q_lens, past_lens=None, scale=None) -> np.ndarray:
+    """Causal GQA attention of new tokens over the cache.  Q [T, H, D] holds
+    the sequences' new tokens back to back (q_lens[b] rows each); token i of
+    sequence b sits at cache row past_lens[b] + i of K/V [B, Hkv, S, D] and
+    attends rows [0, past_lens[b] + i] — per token, the decode formula of
+    ezops/ops/attn_decode.py:64-67 with kv_len = past + i + 1.  fp32 scores,
+    fp64 softmax, output rounded to bf16."""
+    Q, K, V = _f32(Q), _f32(K), _f32(V)
+    T, H, D = Q.shape
+    Hkv = K.shape[1]
+    G = H // Hkv
+    scale = D ** -0.5 if scale is None else scale
+    past_lens = [0] * len(q_lens) if past_lens is None else past_lens
+    out = np.zeros((T, H, D), dtype=np.float32)
+    t0 = 0
+    for b, (n, p) in enumerate(zip(q_lens, past_lens)):
+        L = p + n
+        q = Q[t0:t0 + n].reshape(n, Hkv, G, D).transpose(1, 2, 0, 3)  # [Hkv, G, n, D]
+        s = np.matmul(q, np.swapaxes(K[b, :, :L], -1, -2)[:, None]) * np.float32(scale)  # [Hkv, G, n, L]
+        mask = np.arange(L)[None, :] > (p + np.arange(n))[:, None]
+        s = np.where(mask, -np.inf, s).astype(np.float64)
+        w = np.exp(s - s.max(axis=-1, keepdims=True))
+        w = (w / w.sum(axis=-1, keepdims=True)).astype(np.float32)
+        o = np.matmul(w, V[b, :, :L][:, None])  # [Hkv, G, n, D]
+        out[t0:t0 + n] = o.transpose(2, 0, 1, 3).reshape(n, H, D)
+        t0 += n
+    return bf16(out)
 
 
 def rope_tables(max_seq_len, head_dim, theta=1e6):

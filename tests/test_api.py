@@ -5,13 +5,13 @@ import pytest
 import torch
 
 import oracle
-from ezops import (AttnDecodeOp, FusedOProjFfnOp, FusedQkNormRopeOp, GemvOp, PagedAttnDecodeOp, Qwen3DecodeStepOp,
+from ezops import (AttnDecodeOp, FusedOProjFfnOp, FusedQkNormRopeOp, GemvOp, PagedAttnDecodeOp, PrefillAttnOp, Qwen3DecodeStepOp,
                    Qwen3DenseDecodeOp,
                    ReduceOp, RmsNormOp, SoftmaxOp, get_kernel, list_backends, list_ops, register_kernel)
 from ezops.ops.utils.accuracy import bitwise_equal, sqnr_db
 from ezops.ops.utils.roofline import RooflineResult, measure_roofline
 
-OPS = ["attn_decode", "fused_o_proj_ffn", "fused_qk_norm_rope", "gemv", "paged_attn_decode", "qwen3_decode_step", "qwen3_dense_decode",
+OPS = ["attn_decode", "fused_o_proj_ffn", "fused_qk_norm_rope", "gemv", "paged_attn_decode", "prefill_attn", "qwen3_decode_step", "qwen3_dense_decode",
        "reduce", "rmsnorm", "softmax"]
 
 
@@ -198,3 +198,14 @@ def test_ref_decode_step_vs_oracle_chain(paged):
     assert op.check(logits, torch.from_numpy(logits_ref))
     with pytest.raises(ValueError, match="num_layers"):
         Qwen3DecodeStepOp(1, 64, 128, 192, 4, 32, 0)
+
+
+def test_ref_prefill_attn_vs_oracle():
+    torch.manual_seed(6)
+    op = PrefillAttnOp(2, 8, 2, 32, 64, q_lens=[9, 4], past_lens=[0, 30])
+    Q, K, V = op.gen_data("cpu")
+    out = op(Q, K, V)
+    ref = oracle.prefill_attn(n(Q), n(K), n(V), [9, 4], [0, 30])
+    np.testing.assert_allclose(n(out), ref, rtol=1e-2, atol=1e-2)
+    with pytest.raises(ValueError, match="capacity"):
+        PrefillAttnOp(1, 8, 2, 32, 64, q_lens=[40], past_lens=[30])

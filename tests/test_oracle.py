@@ -212,3 +212,28 @@ def test_qwen3_layer_reference_mode_composition():
     gu = oracle.linear_bf16(xn, Wgu)
     ff = oracle.linear_bf16(oracle.bf16(oracle.bf16(gu[:, :IS] / (1 + np.exp(-gu[:, :IS].astype(np.float64)))) * gu[:, IS:]), Wd)
     np.testing.assert_allclose(out, oracle.bf16(h + ff), rtol=1e-2, atol=1e-2)
+
+
+def test_prefill_attn_pins():
+    """Prefill attention: every token equals the (pinned) decode formula over
+    the cache prefix it may see; a fresh prompt equals torch's causal SDPA."""
+    rng = np.random.default_rng(11)
+    B, H, Hkv, S, D = 2, 4, 2, 40, 16
+    K = rng.standard_normal((B, Hkv, S, D)).astype(np.float32)
+    V = rng.standard_normal((B, Hkv, S, D)).astype(np.float32)
+    q_lens, past = [5, 7], [3, 20]
+    Q = rng.standard_normal((sum(q_lens), H, D)).astype(np.float32)
+    out = oracle.prefill_attn(Q, K, V, q_lens, past)
+    t = 0
+    for b in range(B):
+        for i in range(q_lens[b]):
+            d = oracle.attn_decode(Q[t][None], K[b:b + 1], V[b:b + 1], [past[b] + i + 1])
+            np.testing.assert_allclose(out[t], d[0], rtol=1e-6, atol=1e-6)
+            t += 1
+    n = 9
+    sd = torch.nn.functional.scaled_dot_product_attention(
+        torch.from_numpy(Q[:n]).double().permute(1, 0, 2)[None],
+        torch.from_numpy(np.repeat(K[0, :, :n], 2, axis=0)).double()[None],
+        torch.from_numpy(np.repeat(V[0, :, :n], 2, axis=0)).double()[None], is_causal=True)
+    np.testing.assert_allclose(oracle.prefill_attn(Q[:n], K[:1], V[:1], [n]),
+                               oracle.bf16(sd[0].permute(1, 0, 2).float().numpy()), rtol=1e-2, atol=1e-2)
