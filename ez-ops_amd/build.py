@@ -61,7 +61,9 @@ def build(jobs: int | None = None, verbose: bool = True, extra_flags: tuple = ()
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(lambda src: _compile(src, build_dir, tuple(extra_flags)), sources))
     tmp = lib.with_suffix(".so.tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    rocm_lib = Path(hipcc()).resolve().parent.parent / "lib"
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), f"-L{rocm_lib}",
+           f"-Wl,-rpath,{rocm_lib}", "-lhipblaslt", "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}{r.stderr}")

@@ -253,3 +253,97 @@ extern "C" int ezops_qwen3_decode_step_bf16(const ezops_qwen3_layer* layers, int
   l.epi = kEpiStore; l.xn_ws = static_cast<uint16_t*>(lws);
   return launch_linear(l, s);
 }
+
+// ---------------------------------------------------------------------------
+// Prefill of one Qwen3 dense layer: T new tokens (the sequences' chunks back
+// to back) through RMSNorm -> QKV GEMM -> q/k norm + RoPE + cache write ->
+// causal flash attention -> o_proj GEMM (+residual) -> RMSNorm -> gate/up
+// GEMM -> SwiGLU -> down GEMM (+residual).
+namespace {
+struct PrefillBufs {
+  uint16_t *xn, *qkv, *qn, *att, *h, *gu, *act;
+  void* gemm_ws;
+};
+size_t prefill_ws(const ezops_qwen3_layer* p, int64_t T, PrefillBufs* b, char* base) {
+  const int64_t QR = p->H * p->D, QKV = QR + 2 * p->Hkv * p->D;
+  Carve c{base};
+  auto take = [&](int64_t elems) { return c.take<uint16_t>(size_t(elems) * 2); };
+  PrefillBufs t{};
+  t.xn = take(T * p->HS);
+  t.qkv = take(T * QKV);
+  t.qn = take(T * QR);
+  t.att = take(T * QR);
+  t.h = take(T * p->HS);
+  t.gu = take(T * 2 * p->IS);
+  t.act = take(T * p->IS);
+  t.gemm_ws = c.take<char>(kGemmWorkspace);
+  if (b) *b = t;
+  return size_t(c.p - base);
+}
+}  // namespace
+
+extern "C" size_t ezops_qwen3_prefill_workspace_size(const ezops_qwen3_layer* p, int64_t T) {
+  if (!p || T < 1 || p->H < 1 || p->Hkv < 1 || p->D < 1) return 0;
+  return prefill_ws(p, T, nullptr, nullptr);
+}
+
+extern "C" int ezops_qwen3_prefill_bf16(const ezops_qwen3_layer* p, int64_t T, const int32_t* cu_seqlens,
+                                        int64_t max_q_len, const int32_t* block_table, int64_t num_pages,
+                                        int64_t page_size, void* ws, size_t ws_bytes, hipStream_t s) {
+  EZ_REQUIRE(p && cu_seqlens && ws, "qwen3_prefill: null pointer");
+  EZ_REQUIRE(p->hidden && p->K_cache && p->V_cache && p->Wqkv && p->Wo && p->Wgu && p->Wd && p->out,
+             "qwen3_prefill: null pointer");
+  EZ_REQUIRE(T >= 1 && p->B >= 1 && p->S >= 1 && p->HS >= 1 && p->IS >= 8 && p->IS % 8 == 0 && p->H >= 1 &&
+                 p->Hkv >= 1 && p->H % p->Hkv == 0 && max_q_len >= 1,
+             "qwen3_prefill: bad shape");
+  EZ_REQUIRE((p->cos == nullptr) == (p->sin == nullptr), "qwen3_prefill: cos and sin go together");
+  EZ_REQUIRE(ws_bytes >= ezops_qwen3_prefill_workspace_size(p, T), "qwen3_prefill: workspace too small");
+  if (block_table)
+    EZ_REQUIRE(page_size >= 32 && (page_size & (page_size - 1)) == 0 && p->S % page_size == 0 && num_pages >= 1,
+               "qwen3_prefill: page_size must be a power of two >= 32 dividing S");
+  const int64_t QR = p->H * p->D, KVR = p->Hkv * p->D, QKV = QR + 2 * KVR, HS = p->HS, IS = p->IS;
+  PrefillBufs w{};
+  prefill_ws(p, T, &w, static_cast<char*>(ws));
+  const uint16_t* hidden = static_cast<const uint16_t*>(p->hidden);
+  auto W = [](const void* q) { return static_cast<const uint16_t*>(q); };
+
+  int rc = ezops_rmsnorm_bf16(hidden, p->in_norm_w, w.xn, T, HS, p->eps, s);
+  if (!rc) rc = gemm_bf16(w.xn, HS, W(p->Wqkv), w.qkv, QKV, nullptr, T, QKV, HS, w.gemm_ws, kGemmWorkspace, s);
+  if (rc) return rc;
+
+  QkRopeArgs r{};
+  r.q = w.qkv; r.q_bs = QKV;
+  r.k = w.qkv + QR; r.k_bs = QKV;
+  r.v = w.qkv + QR + KVR; r.v_bs = QKV;
+  r.qw = W(p->q_norm_w); r.kw = W(p->k_norm_w);
+  r.cos = W(p->cos); r.sin = W(p->sin);
+  r.Kc = static_cast<uint16_t*>(p->K_cache); r.Vc = static_cast<uint16_t*>(p->V_cache);
+  r.q_out = w.qn;
+  r.B = T; r.H = p->H; r.Hkv = p->Hkv; r.D = p->D; r.S = p->S;
+  r.cu = cu_seqlens; r.past = p->kv_lens; r.nseq = p->B;
+  r.eps = p->eps;
+  if (block_table) {
+    r.block_table = block_table; r.bt_stride = p->S / page_size; r.page_size = int(page_size);
+    r.num_pages = num_pages;
+  }
+  rc = launch_qk_norm_rope(r, s);
+  if (rc) return rc;
+
+  PrefillAttnArgs a{};
+  a.Q = w.qn; a.q_rs = QR;
+  a.K = r.Kc; a.V = r.Vc;
+  a.Out = w.att; a.o_rs = QR;
+  a.cu = cu_seqlens; a.past = p->kv_lens;
+  a.block_table = block_table; a.bt_stride = r.bt_stride; a.page_size = r.page_size; a.num_pages = num_pages;
+  a.B = p->B; a.H = p->H; a.Hkv = p->Hkv; a.S = p->S; a.D = p->D; a.max_q = max_q_len;
+  a.scale = 0.f;
+  rc = launch_prefill_attn(a, s);
+  if (!rc) rc = gemm_bf16(w.att, QR, W(p->Wo), w.h, HS, hidden, T, HS, QR, w.gemm_ws, kGemmWorkspace, s);
+  if (!rc) rc = ezops_rmsnorm_bf16(w.h, p->post_norm_w, w.xn, T, HS, p->eps, s);
+  if (!rc) rc = gemm_bf16(w.xn, HS, W(p->Wgu), w.gu, 2 * IS, nullptr, T, 2 * IS, HS, w.gemm_ws, kGemmWorkspace, s);
+  if (!rc) rc = launch_silu_mul(w.gu, w.act, T, IS, s);
+  if (!rc)
+    rc = gemm_bf16(w.act, IS, W(p->Wd), static_cast<uint16_t*>(p->out), HS, w.h, T, HS, IS, w.gemm_ws,
+                   kGemmWorkspace, s);
+  return rc;
+}

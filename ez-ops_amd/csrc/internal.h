@@ -62,6 +62,11 @@ struct QkRopeArgs {
   int64_t B, H, Hkv, D, S;
   int64_t position; const int32_t* positions; int64_t pos_offset;
   float eps;
+  // Prefill rows (cu != NULL): row t (t < B) is a token of sequence s with
+  // cu[s] <= t < cu[s+1] (nseq sequences) at cache position past[s] + t - cu[s].
+  const int32_t* cu; const int32_t* past; int64_t nseq;
+  // Paged cache (block_table != NULL): Kc / Vc are pools [pages, Hkv, page_size, D].
+  const int32_t* block_table; int64_t bt_stride; int page_size; int64_t num_pages;
 };
 int launch_qk_norm_rope(const QkRopeArgs& a, hipStream_t s);
 
@@ -105,6 +110,11 @@ struct PrefillAttnArgs {
 };
 int launch_prefill_attn(const PrefillAttnArgs& a, hipStream_t s);
 int launch_silu_mul(const uint16_t* gu, uint16_t* out, int64_t T, int64_t IS, hipStream_t s);
+
+// Library GEMM (hipBLASLt): Y[M,N] = X[M,K] W[N,K]^T (+ R, same layout as Y).
+constexpr size_t kGemmWorkspace = size_t(32) << 20;
+int gemm_bf16(const uint16_t* X, int64_t ldx, const uint16_t* W, uint16_t* Y, int64_t ldy, const uint16_t* R,
+              int64_t M, int64_t N, int64_t K, void* ws, size_t ws_bytes, hipStream_t s);
 
 
 }  // namespace ez

@@ -27,7 +27,18 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QkRopeArgs a) {
   const int64_t kvh = h - a.H;
   const uint16_t* src = is_q ? a.q + b * a.q_bs + h * a.D : a.k + b * a.k_bs + kvh * a.D;
   const uint16_t* w = is_q ? a.qw : a.kw;
-  const int64_t pos = (a.positions ? int64_t(a.positions[b]) : a.position) + a.pos_offset;
+  int64_t seq = b, pos;
+  if (a.cu) {  // prefill row: find its sequence (wave-uniform binary search)
+    int64_t lo = 0, hi = a.nseq - 1;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi + 1) >> 1;
+      if (a.cu[mid] <= b) lo = mid; else hi = mid - 1;
+    }
+    seq = lo;
+    pos = (a.past ? int64_t(a.past[seq]) : 0) + b - a.cu[seq];
+  } else {
+    pos = (a.positions ? int64_t(a.positions[b]) : a.position) + a.pos_offset;
+  }
   const int64_t half = a.D / 2;
   // Positions can come from device memory (per-sequence arrays), so they are
   // range-checked here: an out-of-range position writes nothing.
@@ -46,12 +57,19 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QkRopeArgs a) {
 
   const uint16_t* crow = a.cos ? a.cos + pos * a.D : nullptr;
   const uint16_t* srow = a.sin ? a.sin + pos * a.D : nullptr;
-  uint16_t* dst;
-  if (is_q) {
-    dst = a.q_out + (b * a.H + h) * a.D;
-  } else {
-    dst = a.Kc + ((b * a.Hkv + kvh) * a.S + pos) * a.D;
+  // cache row offset (elements) of (seq, kvh, pos)
+  int64_t crow_off = 0;
+  if (!is_q) {
+    if (a.block_table) {
+      const int sh = __builtin_ctz(unsigned(a.page_size));
+      const int64_t pg = pos >> sh;
+      const uint32_t id = min(uint32_t(a.block_table[seq * a.bt_stride + pg]), uint32_t(a.num_pages - 1));
+      crow_off = ((int64_t(id) * a.Hkv + kvh) * a.page_size + (pos - (pg << sh))) * a.D;
+    } else {
+      crow_off = ((seq * a.Hkv + kvh) * a.S + pos) * a.D;
+    }
   }
+  uint16_t* dst = is_q ? a.q_out + (b * a.H + h) * a.D : a.Kc + crow_off;
   uint16_t* kdst = (!is_q && a.k_out) ? a.k_out + (b * a.Hkv + kvh) * a.D : nullptr;
 #pragma unroll
   for (int t = 0; t < kMaxPairsPerLane; ++t) {
@@ -77,7 +95,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QkRopeArgs a) {
   }
   if (!is_q) {
     const uint16_t* vs = a.v + b * a.v_bs + kvh * a.D;
-    uint16_t* vd = a.Vc + ((b * a.Hkv + kvh) * a.S + pos) * a.D;
+    uint16_t* vd = a.Vc + crow_off;
     for (int64_t i = lane; i < a.D; i += kWave) vd[i] = vs[i];
   }
 }
@@ -90,6 +108,10 @@ int launch_qk_norm_rope(const QkRopeArgs& a, hipStream_t s) {
   EZ_REQUIRE(a.D >= 2 && a.D <= 2 * kMaxPairsPerLane * kWave && a.D % 2 == 0,
              "qk_norm_rope: head_dim must be even and <= %d", 2 * kMaxPairsPerLane * kWave);
   EZ_REQUIRE((a.cos == nullptr) == (a.sin == nullptr), "qk_norm_rope: cos and sin go together");
+  EZ_REQUIRE(!a.cu || a.nseq >= 1, "qk_norm_rope: prefill rows need nseq >= 1");
+  EZ_REQUIRE(!a.block_table || (a.page_size >= 1 && (a.page_size & (a.page_size - 1)) == 0 && a.num_pages >= 1 &&
+                                a.S == a.bt_stride * a.page_size),
+             "qk_norm_rope: paged cache needs a power-of-two page_size and S = max_pages * page_size");
   const int64_t waves = a.B * (a.H + a.Hkv);
   hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(unsigned((waves + 3) / 4)), dim3(256), 0, s, a);
   return launch_status("qk_norm_rope");

@@ -15,6 +15,7 @@ from .ops.paged_attn_decode import PagedAttnDecodeOp
 from .ops.prefill_attn import PrefillAttnOp
 from .ops.qwen3_decode_step import Qwen3DecodeStepOp
 from .ops.qwen3_dense_decode import Qwen3DenseDecodeOp
+from .ops.qwen3_prefill import Qwen3PrefillOp
 from .ops.reduce import ReduceOp
 from .ops.rmsnorm import RmsNormOp
 from .ops.softmax import SoftmaxOp
@@ -22,7 +23,7 @@ from .ops.utils.roofline import RooflineResult
 from .registry import get_kernel, list_backends, list_ops, register_kernel
 
 __all__ = [
-    "AttnDecodeOp", "FusedOProjFfnOp", "FusedQkNormRopeOp", "GemvOp", "Op", "PagedAttnDecodeOp", "PrefillAttnOp", "Qwen3DecodeStepOp", "Qwen3DenseDecodeOp",
-    "ReduceOp", "RmsNormOp", "RooflineResult", "SoftmaxOp", "get_kernel", "list_backends", "list_ops",
-    "register_kernel",
+    "AttnDecodeOp", "FusedOProjFfnOp", "FusedQkNormRopeOp", "GemvOp", "Op", "PagedAttnDecodeOp",
+    "PrefillAttnOp", "Qwen3DecodeStepOp", "Qwen3DenseDecodeOp", "Qwen3PrefillOp", "ReduceOp", "RmsNormOp",
+    "RooflineResult", "SoftmaxOp", "get_kernel", "list_backends", "list_ops", "register_kernel",
 ]

@@ -7,12 +7,14 @@ from .paged_attn_decode import PagedAttnDecodeOp
 from .prefill_attn import PrefillAttnOp
 from .qwen3_decode_step import Qwen3DecodeStepOp
 from .qwen3_dense_decode import Qwen3DenseDecodeOp
+from .qwen3_prefill import Qwen3PrefillOp
 from .reduce import ReduceOp
 from .rmsnorm import RmsNormOp
 from .softmax import SoftmaxOp
 from .utils.roofline import RooflineResult
 
 __all__ = [
-    "AttnDecodeOp", "FusedOProjFfnOp", "FusedQkNormRopeOp", "GemvOp", "Op", "PagedAttnDecodeOp", "PrefillAttnOp", "Qwen3DecodeStepOp", "Qwen3DenseDecodeOp",
-    "ReduceOp", "RmsNormOp", "RooflineResult", "SoftmaxOp",
+    "AttnDecodeOp", "FusedOProjFfnOp", "FusedQkNormRopeOp", "GemvOp", "Op", "PagedAttnDecodeOp",
+    "PrefillAttnOp", "Qwen3DecodeStepOp", "Qwen3DenseDecodeOp", "Qwen3PrefillOp", "ReduceOp", "RmsNormOp",
+    "RooflineResult", "SoftmaxOp",
 ]

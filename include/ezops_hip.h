@@ -244,6 +244,35 @@ int ezops_qwen3_decode_step_bf16(const ezops_qwen3_layer* layers, int64_t n_laye
                                  void* logits, void* workspace, size_t workspace_bytes,
                                  hipStream_t stream);
 
+/* Prefill of one Qwen3 dense layer for a chunk of new tokens.
+ * p->hidden / p->out: [T, HS] bf16, the sequences' new tokens back to back
+ * (sequence b owns rows cu_seqlens[b] .. cu_seqlens[b+1]-1, p->B sequences);
+ * p->kv_lens: rows already cached per sequence before the chunk (NULL = 0);
+ * token i of sequence b is written to cache row kv_lens[b] + i (after q/k
+ * norm + RoPE at that position) and attends rows [0, kv_lens[b] + i].
+ * p->max_kv_len is unused.  block_table != NULL: paged caches as in
+ * ezops_qwen3_dense_decode_paged_bf16.  max_q_len: host bound on the
+ * per-sequence token counts.  D = 128, IS % 8 == 0.  GEMMs run through
+ * hipBLASLt (a shape's first call sets up its algorithm on the host; run it
+ * eagerly once before capturing a graph).
+ * No counterpart in the reference (decode only,
+ * ezops/ops/qwen3_dense_decode.py:9-176): the step that fills the cache the
+ * decode layer reads. */
+size_t ezops_qwen3_prefill_workspace_size(const ezops_qwen3_layer* p, int64_t T);
+int ezops_qwen3_prefill_bf16(const ezops_qwen3_layer* p, int64_t T, const int32_t* cu_seqlens,
+                             int64_t max_q_len, const int32_t* block_table, int64_t num_pages,
+                             int64_t page_size, void* workspace, size_t workspace_bytes,
+                             hipStream_t stream);
+
+/* Library GEMM used by prefill (hipBLASLt): Y[M, N] = X[M, K] W[N, K]^T,
+ * plus R[M, N] (same leading dimension as Y) when R != NULL; bf16 in/out,
+ * fp32 accumulation.  workspace: ezops_gemm_workspace_size() bytes.
+ * No counterpart in the reference (its GEMMs are decode GEMVs). */
+size_t ezops_gemm_workspace_size(void);
+int ezops_gemm_bf16(const void* X, int64_t ldx, const void* W, void* Y, int64_t ldy, const void* R,
+                    int64_t M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
+                    hipStream_t stream);
+
 /* STREAM-style HBM probes used to measure the chip's bandwidth peak
  * (replaces benchmarks/hardware/memory/hbm_saturation.cu:49-90):
  * kind 0 = read (sum into out[0..]; allocates in the caches, used as the

@@ -29,6 +29,8 @@ How each function is pinned (tests/test_oracle.py):
   o_proj_ffn       pure-Python loops (committed golden vectors)
   qwen3_layer      composition of the pinned functions above; pure-Python
                    loops on a tiny layer (committed golden vectors)
+  qwen3_prefill    one token per sequence equals qwen3_layer; a prompt
+                   prefilled in two chunks equals it in one
 """
 
 from __future__ import annotations
@@ -36,8 +38,9 @@ from __future__ import annotations
 import numpy as np
 
 __all__ = [
-    "bf16", "gemv", "linear_bf16", "rmsnorm_f32", "rmsnorm_bf16", "softmax", "reduce_sum",
-    "attn_decode", "paged_to_contiguous", "paged_attn_decode", "prefill_attn", "rope_tables", "qk_norm_rope", "o_proj_ffn", "qwen3_layer",
+    "bf16", "gemv", "linear_bf16", "rmsnorm_f32", "rmsnorm_bf16", "softmax", "reduce_sum", "attn_decode",
+    "paged_to_contiguous", "paged_attn_decode", "prefill_attn", "rope_tables", "qk_norm_rope", "o_proj_ffn",
+    "qwen3_layer", "qwen3_prefill",
 ]
 
 
@@ -259,5 +262,43 @@ def qwen3_layer(hidden, K_cache, V_cache, Wqkv, Wo, Wgu, Wd, num_heads, num_kv_h
     att = attn_decode(qn, Kc, Vc, None if kv_lens is None else lens)
     Wgu = _f32(Wgu)
     out = o_proj_ffn(att.reshape(B, QR), hidden, Wo, post_norm_w if post_norm_w is not None else np.ones(HS, np.float32),
+                     Wgu[:IS], Wgu[IS:], Wd, eps)
+    return out, Kc, Vc
+
+
+def qwen3_prefill(hidden, K_cache, V_cache, Wqkv, Wo, Wgu, Wd, num_heads, num_kv_heads, head_dim, q_lens,
+                  past_lens=None, in_norm_w=None, q_norm_w=None, k_norm_w=None, post_norm_w=None, cos=None,
+                  sin=None, eps=1e-6):
+    """Prefill of a chunk of new tokens through one Qwen3 dense layer: the
+    decode layer's stages (ezops/ops/qwen3_dense_decode.py:142-176) applied to
+    every token, each token's k/v written at cache row past + i of its
+    sequence and its query attending rows [0, past + i] (``prefill_attn``).
+    hidden [T, HS] holds the sequences' tokens back to back.  Returns
+    (out [T, HS], K_cache', V_cache')."""
+    hidden = _f32(hidden)
+    T, HS = hidden.shape
+    D = head_dim
+    QR, KVR = num_heads * D, num_kv_heads * D
+    IS = Wd.shape[1]
+    past_lens = [0] * len(q_lens) if past_lens is None else list(past_lens)
+    seq = np.repeat(np.arange(len(q_lens)), q_lens)
+    pos = np.concatenate([p + np.arange(n) for n, p in zip(q_lens, past_lens)]).astype(np.int64) if T else \
+        np.zeros(0, np.int64)
+    x = rmsnorm_bf16(hidden, in_norm_w, eps)
+    qkv = linear_bf16(x, Wqkv)
+    q = qkv[:, :QR].reshape(T, num_heads, D)
+    k = qkv[:, QR:QR + KVR].reshape(T, num_kv_heads, D)
+    v = qkv[:, QR + KVR:].reshape(T, num_kv_heads, D)
+    ones = np.ones(D, dtype=np.float32)
+    cp = None if cos is None else _f32(cos)[pos][:, None, :]
+    sp = None if sin is None else _f32(sin)[pos][:, None, :]
+    qn = _head_norm_rope(q, ones if q_norm_w is None else q_norm_w, cp, sp, eps)
+    kn = _head_norm_rope(k, ones if k_norm_w is None else k_norm_w, cp, sp, eps)
+    Kc, Vc = _f32(K_cache).copy(), _f32(V_cache).copy()
+    Kc[seq, :, pos, :] = kn
+    Vc[seq, :, pos, :] = _f32(v)
+    att = prefill_attn(qn, Kc, Vc, q_lens, past_lens)
+    Wgu = _f32(Wgu)
+    out = o_proj_ffn(att.reshape(T, QR), hidden, Wo, post_norm_w if post_norm_w is not None else np.ones(HS, np.float32),
                      Wgu[:IS], Wgu[IS:], Wd, eps)
     return out, Kc, Vc

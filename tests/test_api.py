@@ -5,13 +5,13 @@ import pytest
 import torch
 
 import oracle
-from ezops import (AttnDecodeOp, FusedOProjFfnOp, FusedQkNormRopeOp, GemvOp, PagedAttnDecodeOp, PrefillAttnOp, Qwen3DecodeStepOp,
+from ezops import (AttnDecodeOp, FusedOProjFfnOp, FusedQkNormRopeOp, GemvOp, PagedAttnDecodeOp, PrefillAttnOp, Qwen3DecodeStepOp, Qwen3PrefillOp,
                    Qwen3DenseDecodeOp,
                    ReduceOp, RmsNormOp, SoftmaxOp, get_kernel, list_backends, list_ops, register_kernel)
 from ezops.ops.utils.accuracy import bitwise_equal, sqnr_db
 from ezops.ops.utils.roofline import RooflineResult, measure_roofline
 
-OPS = ["attn_decode", "fused_o_proj_ffn", "fused_qk_norm_rope", "gemv", "paged_attn_decode", "prefill_attn", "qwen3_decode_step", "qwen3_dense_decode",
+OPS = ["attn_decode", "fused_o_proj_ffn", "fused_qk_norm_rope", "gemv", "paged_attn_decode", "prefill_attn", "qwen3_decode_step", "qwen3_dense_decode", "qwen3_dense_prefill",
        "reduce", "rmsnorm", "softmax"]
 
 
@@ -209,3 +209,24 @@ def test_ref_prefill_attn_vs_oracle():
     np.testing.assert_allclose(n(out), ref, rtol=1e-2, atol=1e-2)
     with pytest.raises(ValueError, match="capacity"):
         PrefillAttnOp(1, 8, 2, 32, 64, q_lens=[40], past_lens=[30])
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_ref_prefill_layer_vs_oracle(paged):
+    torch.manual_seed(8)
+    kw = dict(page_size=32, num_pages=5) if paged else {}
+    op = Qwen3PrefillOp(2, 64, 128, 192, 4, 32, q_lens=[9, 3], past_lens=[0, 40], num_kv_heads=2,
+                        norm_weights=True, rope_theta=1e6, **kw)
+    data = op.gen_data("cpu")
+    npy = [n(x) for x in data]
+    K0, V0 = npy[1], npy[2]
+    if paged:
+        bt = data[-1].numpy()
+        K0, V0 = oracle.paged_to_contiguous(K0, bt, 32), oracle.paged_to_contiguous(V0, bt, 32)
+    out = op(*data)
+    ref, Kc, Vc = oracle.qwen3_prefill(npy[0], K0, V0, *npy[3:7], 4, 2, 32, [9, 3], [0, 40], in_norm_w=npy[7],
+                                       q_norm_w=npy[8], k_norm_w=npy[9], post_norm_w=npy[10], cos=npy[11],
+                                       sin=npy[12])
+    assert op.check(out, torch.from_numpy(ref))
+    K1 = n(data[1]) if not paged else oracle.paged_to_contiguous(n(data[1]), bt, 32)
+    np.testing.assert_allclose(K1, Kc, rtol=1e-2, atol=1e-2)

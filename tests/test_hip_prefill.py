@@ -47,3 +47,82 @@ def test_prefill_attn_paged_equals_contiguous(page_size):
     cop = PrefillAttnOp(B, 32, 8, 128, S, q_lens, past, backend="hip")
     K, V = paged_to_contiguous(Kp, bt).contiguous(), paged_to_contiguous(Vp, bt).contiguous()
     assert torch.equal(out, cop(Q, K, V))
+
+
+# ---- prefill layer and its library GEMM
+from ezops import Qwen3DenseDecodeOp, Qwen3PrefillOp, _hip  # noqa: E402
+
+QWEN3_8B = dict(hidden_size=4096, intermediate_size=12288, num_heads=32, head_dim=128)
+
+
+@pytest.mark.parametrize("M,N,K,resid", [(512, 6144, 4096, False), (77, 4096, 12288, True), (1, 200, 64, True)])
+def test_gemm_vs_oracle(M, N, K, resid):
+    rng = np.random.default_rng(M + N)
+    X = oracle.bf16(rng.standard_normal((M, K)).astype(np.float32))
+    W = oracle.bf16(rng.standard_normal((N, K)).astype(np.float32) * K ** -0.5)
+    R = oracle.bf16(rng.standard_normal((M, N)).astype(np.float32))
+    g = lambda a: torch.from_numpy(a).to(torch.bfloat16).cuda()  # noqa: E731
+    Xg, Wg, Rg = g(X), g(W), g(R)
+    Y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(_hip.size("ezops_gemm_workspace_size"), dtype=torch.uint8, device="cuda")
+    _hip.call("ezops_gemm_bf16", Xg.data_ptr(), K, Wg.data_ptr(), Y.data_ptr(), N, Rg.data_ptr() if resid else None,
+              M, N, K, ws.data_ptr(), ws.numel(), _hip.stream())
+    ref = oracle.linear_bf16(X, W) + (R if resid else 0)
+    np.testing.assert_allclose(n(Y), ref, **BF_TOL)
+
+
+def _prefill_ref(op, data, paged):
+    npy = [n(x) for x in data]
+    K0, V0 = npy[1], npy[2]
+    if paged:
+        bt = data[-1].cpu().numpy()
+        K0, V0 = oracle.paged_to_contiguous(K0, bt, op.page_size), oracle.paged_to_contiguous(V0, bt, op.page_size)
+    return oracle.qwen3_prefill(npy[0], K0, V0, *npy[3:7], op.num_heads, op.num_kv_heads, op.head_dim, op.q_lens,
+                                op.past_lens, in_norm_w=npy[7], q_norm_w=npy[8], k_norm_w=npy[9],
+                                post_norm_w=npy[10], cos=npy[11], sin=npy[12])
+
+
+@pytest.mark.parametrize("q_lens,past,S", [([512], [0], 1024), ([100, 1, 257], [0, 600, 300], 1024)])
+def test_qwen3_prefill_vs_oracle(q_lens, past, S):
+    torch.manual_seed(len(q_lens))
+    op = Qwen3PrefillOp(len(q_lens), S, q_lens=q_lens, past_lens=past, backend="hip", num_kv_heads=8,
+                        norm_weights=True, rope_theta=1e6, **QWEN3_8B)
+    data = op.gen_data()
+    K0, V0 = data[1].clone(), data[2].clone()
+    ref, Kc, Vc = _prefill_ref(op, (data[0], K0, V0, *data[3:]), False)
+    out = op(*data)
+    ref_t = torch.from_numpy(ref).cuda()
+    assert op.check(out, ref_t), (out.float() - ref_t).norm().item() / ref_t.norm().item()
+    np.testing.assert_allclose(n(data[1]), Kc, **BF_TOL)
+    np.testing.assert_allclose(n(data[2]), Vc, **BF_TOL)  # V rows are QKV GEMM outputs
+
+
+def test_qwen3_prefill_paged_equals_contiguous_then_decode():
+    """Paged prefill equals contiguous prefill bit-for-bit (output and cache);
+    the decode layer then continues from the prefilled cache."""
+    q_lens, past, S, P = [300, 45], [0, 100], 1024, 64
+    torch.manual_seed(3)
+    pop = Qwen3PrefillOp(2, S, q_lens=q_lens, past_lens=past, backend="hip", num_kv_heads=8, norm_weights=True,
+                         rope_theta=1e6, page_size=P, **QWEN3_8B)
+    data = list(pop.gen_data())
+    bt = data[-1]
+    Kc = paged_to_contiguous(data[1], bt).contiguous()
+    Vc = paged_to_contiguous(data[2], bt).contiguous()
+    out = pop(*data)
+    cop = Qwen3PrefillOp(2, S, q_lens=q_lens, past_lens=past, backend="hip", num_kv_heads=8, norm_weights=True,
+                         rope_theta=1e6, **QWEN3_8B)
+    cout = cop(data[0], Kc, Vc, *data[3:-1])
+    assert torch.equal(out, cout)
+    assert torch.equal(paged_to_contiguous(data[1], bt), Kc) and torch.equal(paged_to_contiguous(data[2], bt), Vc)
+    # one decode step on top of the prefilled (paged) cache vs the oracle
+    lens = [p + q + 1 for p, q in zip(past, q_lens)]
+    dop = Qwen3DenseDecodeOp(2, S, backend="hip", num_kv_heads=8, kv_lens=lens, norm_weights=True, rope_theta=1e6,
+                             page_size=P, **QWEN3_8B)
+    hid = torch.randn(2, 4096, device="cuda").to(torch.bfloat16)
+    K_before = paged_to_contiguous(data[1], bt).cpu().float().numpy()
+    V_before = paged_to_contiguous(data[2], bt).cpu().float().numpy()
+    dout = dop(hid, data[1], data[2], *data[3:])
+    npw = [n(x) for x in data[3:13]]
+    ref, _, _ = oracle.qwen3_layer(n(hid), K_before, V_before, *npw[:4], 32, 8, 128, kv_lens=lens, in_norm_w=npw[4],
+                                   q_norm_w=npw[5], k_norm_w=npw[6], post_norm_w=npw[7], cos=npw[8], sin=npw[9])
+    assert dop.check(dout, torch.from_numpy(ref).cuda())

@@ -237,3 +237,32 @@ def test_prefill_attn_pins():
         torch.from_numpy(np.repeat(V[0, :, :n], 2, axis=0)).double()[None], is_causal=True)
     np.testing.assert_allclose(oracle.prefill_attn(Q[:n], K[:1], V[:1], [n]),
                                oracle.bf16(sd[0].permute(1, 0, 2).float().numpy()), rtol=1e-2, atol=1e-2)
+
+
+def test_qwen3_prefill_pins():
+    """Prefill layer: one new token per sequence over a cached prefix is the
+    (pinned) decode layer; a prompt prefilled in two chunks equals one chunk
+    (outputs and cache)."""
+    rng = np.random.default_rng(12)
+    B, S, HS, IS, H, Hkv, D = 2, 32, 64, 96, 4, 2, 16
+    w = lambda *s: oracle.bf16(rng.standard_normal(s).astype(np.float32) * s[-1] ** -0.5)  # noqa: E731
+    Wqkv, Wo, Wgu, Wd = w((H + 2 * Hkv) * D, HS), w(HS, H * D), w(2 * IS, HS), w(HS, IS)
+    K = oracle.bf16(rng.standard_normal((B, Hkv, S, D)).astype(np.float32))
+    V = oracle.bf16(rng.standard_normal((B, Hkv, S, D)).astype(np.float32))
+    cos, sin = oracle.rope_tables(S, D)
+    nw = dict(in_norm_w=1 + 0.1 * w(HS), q_norm_w=1 + 0.1 * w(D), k_norm_w=1 + 0.1 * w(D), post_norm_w=1 + 0.1 * w(HS))
+    hid = oracle.bf16(rng.standard_normal((B, HS)).astype(np.float32))
+    lens = [20, 7]
+    out_p, Kp, Vp = oracle.qwen3_prefill(hid, K, V, Wqkv, Wo, Wgu, Wd, H, Hkv, D, [1, 1], [l - 1 for l in lens],
+                                         cos=cos, sin=sin, **nw)
+    out_d, Kd, Vd = oracle.qwen3_layer(hid, K, V, Wqkv, Wo, Wgu, Wd, H, Hkv, D, kv_lens=lens, cos=cos, sin=sin, **nw)
+    np.testing.assert_allclose(out_p, out_d, rtol=1e-6, atol=1e-6)
+    np.testing.assert_array_equal(Kp, Kd)
+    np.testing.assert_array_equal(Vp, Vd)
+    prompt = oracle.bf16(rng.standard_normal((12, HS)).astype(np.float32))
+    one, K1, V1 = oracle.qwen3_prefill(prompt, K[:1], V[:1], Wqkv, Wo, Wgu, Wd, H, Hkv, D, [12], cos=cos, sin=sin, **nw)
+    a, Ka, Va = oracle.qwen3_prefill(prompt[:5], K[:1], V[:1], Wqkv, Wo, Wgu, Wd, H, Hkv, D, [5], cos=cos, sin=sin, **nw)
+    b, Kb, Vb = oracle.qwen3_prefill(prompt[5:], Ka, Va, Wqkv, Wo, Wgu, Wd, H, Hkv, D, [7], [5], cos=cos, sin=sin, **nw)
+    np.testing.assert_allclose(np.concatenate([a, b]), one, rtol=1e-6, atol=1e-6)
+    np.testing.assert_array_equal(Kb, K1)
+    np.testing.assert_array_equal(Vb, V1)
