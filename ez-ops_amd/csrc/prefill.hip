@@ -2,17 +2,18 @@
 // cache for a chunk of new tokens per sequence, and the SwiGLU elementwise
 // stage of the batched FFN.
 //
-// Attention layout on the matrix cores (v_mfma_f32_16x16x32_bf16, lane 16g+i
-// holds A[i][8g..8g+7], B[8g..8g+7][i]; C[4g+r][i] in lane 16g+i, reg r):
-//   S^T = K Q^T   A = 16 keys x 32 dims of K (LDS, XOR-swizzled rows),
+// Attention layout on the matrix cores (v_mfma_f32_32x32x16_bf16: lane
+// 32h+i holds A[i][8h..8h+7] and B[8h..8h+7][i]; reg r of lane 32h+j holds
+// C[8(r/4) + 4h + r%4][j]):
+//   S^T = K Q^T   A = 32 keys x 16 dims of K (LDS, XOR-swizzled rows),
 //                 B = Q^T (registers, loaded once), C = S^T[key][query]
 //   O^T = V^T P^T A = V^T (LDS, stored transposed), B = P^T straight from the
-//                 S^T registers: the k slots 8g..8g+7 of a 32-key step are
-//                 keys 4g..4g+3 of its two 16-key tiles, the same slot order
+//                 S^T registers: the k slots 8h..8h+7 of a 16-key step are
+//                 keys 4h..4h+3 and 8+4h..8+4h+3 of it, the same slot order
 //                 in A and B, so P never leaves the lane.
 // Queries sit in the lane column j in both products, so a query's running
 // max / sum and its output column share the lane: the only cross-lane step
-// is the 4-row reduction over the lanes j, j+16, j+32, j+48.
+// is the swap between the lane halves j and j+32.
 #include "common.h"
 #include "internal.h"
 #include "status.h"
@@ -22,18 +23,29 @@ namespace ez {
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kPD = 128;         // head dim
-constexpr int kPW = 8;           // waves per block
-constexpr int kBK = 64;          // keys per tile
-constexpr int kVtStride = kBK + 4;  // transposed V row stride (elements), padded against bank conflicts
+constexpr int kPD = 128;            // head dim
+constexpr int kPW = 4;              // waves per block
+constexpr int kBK = 64;             // keys per tile
+constexpr int kVtStride = kBK + 4;  // transposed V row stride (elements): 8-byte aligned, padded
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-__device__ __forceinline__ float group4_max(float v) {
-  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
-  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+// Two fp32 -> packed bf16 in one hardware convert (round to nearest even).
+__device__ __forceinline__ uint32_t cvt_bf2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
+}
+
+// Value of the other lane half (lane l ^ 32) combined with this lane's.
+__device__ __forceinline__ float halves_max(float v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float halves_sum(float v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
 
 // Address of cache row `row` of (sequence b, kv head) for the staging loads.
@@ -47,18 +59,23 @@ __device__ __forceinline__ const uint16_t* cache_row(const PrefillAttnArgs& a, c
   return base + ((int64_t(id) * a.Hkv + kvh) * a.page_size + (row - (pg << sh))) * kPD;
 }
 
-// Block = (query tile, sequence, kv head); wave w serves query head
-// kvh*G + w%G, query rows 16*(w/G) .. +15 of the tile (BQ = 16*kPW/G rows).
+// Block = (query tile, sequence, kv head, head group of HPB = min(G, 4) query
+// heads); wave w serves query head kvh*G + hb*HPB + w%HPB, query rows
+// 32*(w/HPB) .. +31 of the tile (BQ = 32 * 4/HPB rows).  K/V tiles of 64
+// keys are double-buffered in LDS (one barrier per tile).
 template <int G, bool PAGED>
-__global__ __launch_bounds__(kPW * kWave) void prefill_attn_kernel(PrefillAttnArgs a, int ntq) {
-  constexpr int QW = kPW / G;  // 16-row query groups per head
-  constexpr int BQ = 16 * QW;
-  __shared__ __align__(16) uint16_t Ks[kBK * kPD];        // [key][16B chunk ^ (key & 15)]
-  __shared__ __align__(16) uint16_t Vt[kPD * kVtStride];  // [dim][key]
+__global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))) void prefill_attn_kernel(PrefillAttnArgs a, int ntq) {
+  constexpr int HPB = G < 4 ? G : 4;
+  constexpr int NHB = G / HPB;  // head groups per kv head
+  constexpr int BQ = 32 * (kPW / HPB);
+  __shared__ __align__(16) uint16_t Ks[2][kBK * kPD];        // [key][16B chunk ^ (key & 15)]
+  __shared__ __align__(16) uint16_t Vt[2][kPD * kVtStride];  // [dim][key]
 
-  const int bh = int(a.B * a.Hkv);
-  const int qt = ntq - 1 - int(blockIdx.x) / bh;  // longest (last) query tiles first
-  const int rem = int(blockIdx.x) % bh;
+  const int per_q = int(a.B * a.Hkv) * NHB;
+  const int qt = ntq - 1 - int(blockIdx.x) / per_q;  // longest (last) query tiles first
+  int rem = int(blockIdx.x) % per_q;
+  const int hb = rem % NHB;
+  rem /= NHB;
   const int b = rem / int(a.Hkv), kvh = rem % int(a.Hkv);
   const int64_t q0 = a.cu[b];
   const int64_t qlen0 = int64_t(a.cu[b + 1]) - q0;
@@ -68,136 +85,152 @@ __global__ __launch_bounds__(kPW * kWave) void prefill_attn_kernel(PrefillAttnAr
   if (int64_t(qt) * BQ >= qlen) return;
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
-  const int g = lane >> 4, j = lane & 15;
-  const int hq = kvh * G + wave % G;
-  const int64_t qi0 = int64_t(qt) * BQ + (wave / G) * 16;  // first query row (in the sequence) of this wave
-  const int64_t qrow = min(qi0 + j, qlen - 1);              // clamped: rows past qlen compute, never store
-  const int64_t qpos = past + qrow;                         // its cache position
-  const int64_t wave_last = past + min(qi0 + 15, qlen - 1);
+  const int h = lane >> 5, j = lane & 31;
+  const int hq = kvh * G + hb * HPB + wave % HPB;
+  const int64_t qi0 = int64_t(qt) * BQ + (wave / HPB) * 32;  // first query row (in the sequence) of this wave
+  const int64_t qrow = min(qi0 + j, qlen - 1);               // clamped: rows past qlen compute, never store
+  const int64_t qpos = past + qrow;                          // its cache position
+  const int64_t wave_last = past + min(qi0 + 31, qlen - 1);
   const int64_t kend = past + min(int64_t(qt + 1) * BQ, qlen);  // keys [0, kend) serve this block
   const float sl2 = a.scale * kLog2e;
 
-  bf16x8_t qf[kPD / 32];
+  bf16x8_t qf[kPD / 16];
   {
-    const uint16_t* qp = a.Q + (q0 + qrow) * a.q_rs + int64_t(hq) * kPD;
+    const uint16_t* qp = a.Q + (q0 + qrow) * a.q_rs + int64_t(hq) * kPD + 8 * h;
 #pragma unroll
-    for (int s = 0; s < kPD / 32; ++s) qf[s] = as_bf16x8(*reinterpret_cast<const uint4*>(qp + 32 * s + 8 * g));
+    for (int s = 0; s < kPD / 16; ++s) qf[s] = as_bf16x8(*reinterpret_cast<const uint4*>(qp + 16 * s));
   }
 
-  f32x4_t o[kPD / 16];
+  f32x16_t o[kPD / 32];
 #pragma unroll
-  for (int d = 0; d < kPD / 16; ++d) o[d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int d = 0; d < kPD / 32; ++d)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[d][r] = 0.f;
   float m = -INFINITY, l = 0.f;
 
-  // staging assignment: K chunks id = tid + 512c -> key id/16, chunk id%16;
-  // V: key pair tid/16, dim chunk tid%16
-  uint4 kr[2], vr[2];
-  const int vkp = tid >> 4, vcc = tid & 15;
+  // staging: K chunks id = tid + 256c -> key id/16, chunk id%16; V: keys
+  // 4*vm .. 4*vm+3 (vm = tid/16), dims 8*vc .. 8*vc+7 (vc = tid%16)
+  uint4 kr[4], vr[4];
+  const int vm = tid >> 4, vc = tid & 15;
   auto load_tile = [&](int64_t k0) {
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
+    for (int c = 0; c < 4; ++c) {
       const int id = tid + c * kPW * kWave;
       const int64_t row = min(k0 + (id >> 4), kend - 1);
       kr[c] = *reinterpret_cast<const uint4*>(cache_row<PAGED>(a, a.K, b, kvh, row) + (id & 15) * 8);
-      const int64_t vrow = min(k0 + 2 * vkp + c, kend - 1);
-      vr[c] = *reinterpret_cast<const uint4*>(cache_row<PAGED>(a, a.V, b, kvh, vrow) + vcc * 8);
+      const int64_t vrow = min(k0 + 4 * vm + c, kend - 1);
+      vr[c] = *reinterpret_cast<const uint4*>(cache_row<PAGED>(a, a.V, b, kvh, vrow) + vc * 8);
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int id = tid + c * kPW * kWave;
+      const int r = id >> 4, cc = id & 15;
+      *reinterpret_cast<uint4*>(&Ks[buf][r * kPD + ((cc ^ (r & 15)) * 8)]) = kr[c];
+    }
+    const uint32_t* v0 = reinterpret_cast<const uint32_t*>(&vr[0]);
+    const uint32_t* v1 = reinterpret_cast<const uint32_t*>(&vr[1]);
+    const uint32_t* v2 = reinterpret_cast<const uint32_t*>(&vr[2]);
+    const uint32_t* v3 = reinterpret_cast<const uint32_t*>(&vr[3]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int sh = (e & 1) * 16;
+      const uint32_t k0v = (v0[e >> 1] >> sh) & 0xffffu, k1v = (v1[e >> 1] >> sh) & 0xffffu;
+      const uint32_t k2v = (v2[e >> 1] >> sh) & 0xffffu, k3v = (v3[e >> 1] >> sh) & 0xffffu;
+      *reinterpret_cast<uint2*>(&Vt[buf][(vc * 8 + e) * kVtStride + 4 * vm]) =
+          make_uint2(k0v | (k1v << 16), k2v | (k3v << 16));
     }
   };
   load_tile(0);
+  store_tile(0);
+  __syncthreads();
 
-  for (int64_t k0 = 0; k0 < kend; k0 += kBK) {
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int id = tid + c * kPW * kWave;
-      const int r = id >> 4, cc = id & 15;
-      *reinterpret_cast<uint4*>(&Ks[r * kPD + ((cc ^ (r & 15)) * 8)]) = kr[c];
-    }
-    {
-      const uint32_t* v0 = reinterpret_cast<const uint32_t*>(&vr[0]);
-      const uint32_t* v1 = reinterpret_cast<const uint32_t*>(&vr[1]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t lo = (e & 1) ? (v0[e >> 1] >> 16) : (v0[e >> 1] & 0xffffu);
-        const uint32_t hi = (e & 1) ? (v1[e >> 1] >> 16) : (v1[e >> 1] & 0xffffu);
-        *reinterpret_cast<uint32_t*>(&Vt[(vcc * 8 + e) * kVtStride + 2 * vkp]) = lo | (hi << 16);
-      }
-    }
-    __syncthreads();
-    if (k0 + kBK < kend) load_tile(k0 + kBK);  // next tile's global loads overlap this tile's math
+  int buf = 0;
+  for (int64_t k0 = 0; k0 < kend; k0 += kBK, buf ^= 1) {
+    const bool more = k0 + kBK < kend;
+    if (more) load_tile(k0 + kBK);  // next tile's global loads overlap this tile's math
 
     if (k0 <= wave_last) {  // a wave whose queries all precede the tile skips it
-      f32x4_t st[kBK / 16];
+      f32x16_t st[kBK / 32];
 #pragma unroll
-      for (int t = 0; t < kBK / 16; ++t) {
-        st[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        const int r = 16 * t + j;  // key row read by this lane (A operand row i = j)
+      for (int kk = 0; kk < kBK / 32; ++kk) {
 #pragma unroll
-        for (int s = 0; s < kPD / 32; ++s) {
-          const uint4 kv = *reinterpret_cast<const uint4*>(&Ks[r * kPD + (((4 * s + g) ^ (r & 15)) * 8)]);
-          st[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kv), qf[s], st[t], 0, 0, 0);
+        for (int r = 0; r < 16; ++r) st[kk][r] = 0.f;
+        const int row = 32 * kk + j;  // key row read by this lane (A operand row i = j)
+#pragma unroll
+        for (int s = 0; s < kPD / 16; ++s) {
+          const uint4 kv = *reinterpret_cast<const uint4*>(&Ks[buf][row * kPD + (((2 * s + h) ^ (row & 15)) * 8)]);
+          st[kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kv), qf[s], st[kk], 0, 0, 0);
         }
       }
-      // st[t][r] = S[query j][key k0 + 16t + 4g + r]
+      // st[kk][r] = S[query j][key k0 + 32kk + 8(r/4) + 4h + r%4] (unscaled)
+      if (k0 + kBK - 1 > past + qi0) {  // diagonal tile: causal mask (32-bit offsets)
+        const int lim = int(qpos - k0) - 4 * h;
+#pragma unroll
+        for (int kk = 0; kk < kBK / 32; ++kk)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (32 * kk + 8 * (r >> 2) + (r & 3) > lim) st[kk][r] = -INFINITY;
+      }
       float mx = -INFINITY;
 #pragma unroll
-      for (int t = 0; t < kBK / 16; ++t)
+      for (int kk = 0; kk < kBK / 32; ++kk)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int64_t kp = k0 + 16 * t + 4 * g + r;
-          const float sv = kp <= qpos ? st[t][r] * sl2 : -INFINITY;
-          st[t][r] = sv;
-          mx = fmaxf(mx, sv);
-        }
-      mx = group4_max(mx);
-      const float mn = fmaxf(m, mx);  // finite: key 0 is visible to every query
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[kk][r]);
+      mx = halves_max(mx);
+      const float mn = fmaxf(m, mx * sl2);  // finite: key 0 is visible to every query
       const float alpha = exp2f(m - mn);
       m = mn;
       l *= alpha;
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // rescale only when some row max moved
 #pragma unroll
-      for (int d = 0; d < kPD / 16; ++d) o[d] *= alpha;
-      bf16x8_t pb[kBK / 32];
-#pragma unroll
-      for (int u = 0; u < kBK / 32; ++u) {
-        uint32_t w[4];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          float p[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            p[r] = exp2f(st[2 * u + h][r] - mn);
-            l += p[r];
-          }
-          w[2 * h] = pack_bf2(p[0], p[1]);
-          w[2 * h + 1] = pack_bf2(p[2], p[3]);
-        }
-        pb[u] = as_bf16x8(make_uint4(w[0], w[1], w[2], w[3]));
+        for (int d = 0; d < kPD / 32; ++d) o[d] *= alpha;
       }
 #pragma unroll
-      for (int d = 0; d < kPD / 16; ++d) {
-        const uint16_t* vrow = &Vt[(16 * d + j) * kVtStride];
+      for (int kk = 0; kk < kBK / 32; ++kk) {
 #pragma unroll
-        for (int u = 0; u < kBK / 32; ++u) {
-          const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 32 * u + 4 * g);
-          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 32 * u + 16 + 4 * g);
-          o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y)), pb[u],
-                                                         o[d], 0, 0, 0);
+        for (int u = 0; u < 2; ++u) {
+          // k step of 16 keys (k0 + 32kk + 16u ..): slots 8h..8h+7 = regs 8u..8u+7
+          uint32_t w[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float p0 = exp2f(fmaf(st[kk][8 * u + 2 * q], sl2, -mn));
+            const float p1 = exp2f(fmaf(st[kk][8 * u + 2 * q + 1], sl2, -mn));
+            l += p0 + p1;
+            w[q] = cvt_bf2(p0, p1);
+          }
+          const bf16x8_t pb = as_bf16x8(make_uint4(w[0], w[1], w[2], w[3]));
+          const int kc = 32 * kk + 16 * u + 4 * h;
+#pragma unroll
+          for (int d = 0; d < kPD / 32; ++d) {
+            const uint16_t* vrow = &Vt[buf][(32 * d + j) * kVtStride + kc];
+            const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
+            const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
+            o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y)), pb,
+                                                           o[d], 0, 0, 0);
+          }
         }
       }
     }
+    if (more) store_tile(buf ^ 1);
     __syncthreads();
   }
 
-  // l: this lane's share of query j's sum; the four lanes j + 16g add up.
-  l = rowgroup_sum<16>(l);
+  // l: this lane's share of query j's sum; the two lane halves add up.
+  l = halves_sum(l);
   if (qi0 + j < qlen) {
     const float inv = 1.f / l;
-    uint16_t* op = a.Out + (q0 + qi0 + j) * a.o_rs + int64_t(hq) * kPD + 4 * g;
+    uint16_t* op = a.Out + (q0 + qi0 + j) * a.o_rs + int64_t(hq) * kPD + 4 * h;
 #pragma unroll
-    for (int d = 0; d < kPD / 16; ++d) {
-      // o[d][r] = O^T[dim 16d + 4g + r][query j]
-      *reinterpret_cast<uint2*>(op + 16 * d) =
-          make_uint2(pack_bf2(o[d][0] * inv, o[d][1] * inv), pack_bf2(o[d][2] * inv, o[d][3] * inv));
-    }
+    for (int d = 0; d < kPD / 32; ++d)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        // o[d][4q + e] = O^T[dim 32d + 8q + 4h + e][query j]
+        *reinterpret_cast<uint2*>(op + 32 * d + 8 * q) =
+            make_uint2(cvt_bf2(o[d][4 * q] * inv, o[d][4 * q + 1] * inv),
+                       cvt_bf2(o[d][4 * q + 2] * inv, o[d][4 * q + 3] * inv));
+      }
   }
 }
 
@@ -239,9 +272,10 @@ int launch_prefill_attn(const PrefillAttnArgs& a, hipStream_t s) {
   if (a.max_q == 0) return 0;
   PrefillAttnArgs aa = a;
   if (aa.scale <= 0.f) aa.scale = 1.f / sqrtf(float(kPD));
-  const int bq = 16 * kPW / int(G);
+  const int hpb = G < 4 ? int(G) : 4;
+  const int bq = 32 * kPW / hpb;
   const int ntq = int((a.max_q + bq - 1) / bq);
-  const int64_t blocks = int64_t(ntq) * a.B * a.Hkv;
+  const int64_t blocks = int64_t(ntq) * a.B * a.Hkv * (G / hpb);
   EZ_REQUIRE(blocks < (int64_t(1) << 31), "prefill_attn: grid too large");
   const dim3 grid{unsigned(blocks)}, block{unsigned(kPW * kWave)};
 #define EZ_PF(GG)                                                                                    \
