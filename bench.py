@@ -32,6 +32,7 @@ for _p in (ROOT, ROOT / "ez-ops_amd"):
 
 METRIC = "sol-score (achieved/peak HBM GB/s) + µs per Qwen3-8B decode layer, bs=1"
 SPEC_HBM_GBPS = 8000.0  # MI355X published HBM3E bandwidth
+SPEC_BF16_TFLOPS = 2500.0  # MI355X published dense bf16 MFMA peak
 QWEN3_8B = dict(hidden_size=4096, intermediate_size=12288, num_heads=32, head_dim=128, num_kv_heads=8)
 SEQ_MAX = 16384
 STACK = 4  # distinct layers per timed graph replay
@@ -140,6 +141,54 @@ def decode_step(torch, data, lens, batch: int, steps: int, warmup: int, flush) -
             "achieved_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "timing": "HIP events around each graph replay of the whole step (36 layers + LM head), "
                       "1 GiB read flush between replays"}
+
+
+def prefill(torch, flush) -> dict:
+    """Prefill (the step before decode): one Qwen3-8B layer over a fresh
+    4096-token prompt (hipBLASLt GEMMs + causal MFMA flash attention + cache
+    write), and the attention kernel alone at 4K and 16K tokens, against the
+    dense bf16 MFMA peak.  HIP events around each call, median of 5."""
+    from ezops import PrefillAttnOp, Qwen3PrefillOp
+
+    def timed(fn, reps=5):
+        for _ in range(2):
+            fn()
+        ts = []
+        for _ in range(reps):
+            flush()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b))
+        return statistics.median(ts)
+
+    out = {}
+    T = 4096
+    op = Qwen3PrefillOp(1, T, q_lens=[T], backend="hip", norm_weights=True, rope_theta=1e6, **QWEN3_8B)
+    torch.manual_seed(0)
+    data = [t.cuda() for t in op.gen_data("cpu")]
+    ms = timed(lambda: op(*data))
+    gemm = 2 * T * (6144 * 4096 + 4096 * 4096 + 24576 * 4096 + 4096 * 12288)
+    attn = 2 * T * T * 128 * 32  # causal: two T x T/2 x 128 products per head
+    out["layer_T4096"] = {"ms": round(ms, 3), "tokens_per_s": round(T / ms * 1e3),
+                          "TFLOPs": round((gemm + attn) / ms / 1e9, 1),
+                          "frac_of_bf16_peak": round((gemm + attn) / ms / 1e9 / SPEC_BF16_TFLOPS, 4)}
+    del data
+    for T in (4096, 16384):
+        at = PrefillAttnOp(1, 32, 8, 128, T, [T], backend="hip")
+        Q = torch.randn(T, 32, 128, device="cuda").to(torch.bfloat16)
+        K = torch.randn(1, 8, T, 128, device="cuda").to(torch.bfloat16)
+        V = torch.randn(1, 8, T, 128, device="cuda").to(torch.bfloat16)
+        ms = timed(lambda: at(Q, K, V))
+        fl = 2 * T * T * 128 * 32
+        out[f"attention_T{T}"] = {"kernel": "prefill_attn_kernel<4, false>", "bound": "mfma", "us": round(ms * 1e3, 1),
+                                  "TFLOPs": round(fl / ms / 1e9, 1),
+                                  "frac_of_bf16_peak": round(fl / ms / 1e9 / SPEC_BF16_TFLOPS, 4)}
+        del Q, K, V
+    torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(torch, op, data, lens, budget_s: float = 20.0) -> dict:
@@ -274,8 +323,18 @@ def profile_only(torch, _hip, flush, args) -> int:
     copy:    ezops_hbm_probe copy of 256 MiB (256 MiB read + 256 MiB written): the
              calibration kernel for FETCH_SIZE / WRITE_SIZE.
     layer:   one full B=1 layer step.
+    prefill: one Qwen3-8B layer prefill over a fresh 4096-token prompt.
     """
-    if args.profile_kernel == "copy":  # no flush in between: every probe dispatch is a 256 MiB copy
+    if args.profile_kernel == "prefill":
+        from ezops import Qwen3PrefillOp
+
+        op = Qwen3PrefillOp(1, 4096, q_lens=[4096], backend="hip", norm_weights=True, rope_theta=1e6, **QWEN3_8B)
+        torch.manual_seed(0)
+        data = [t.cuda() for t in op.gen_data("cpu")]
+        for _ in range(10):
+            flush()
+            op(*data)
+    elif args.profile_kernel == "copy":  # no flush in between: every probe dispatch is a 256 MiB copy
         n = (256 << 20) // 4
         a = torch.empty(n, device="cuda")
         b = torch.rand(n, device="cuda")
@@ -309,8 +368,9 @@ def main() -> int:
     ap.add_argument("--no-ops", action="store_true", help="skip the per-op table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-step", action="store_true", help="skip the 36-layer decode-step timing")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill timings")
     ap.add_argument("--batch", type=int, default=1, help="layer batch (headline is 1)")
-    ap.add_argument("--profile-kernel", choices=["gate_up", "copy", "layer"],
+    ap.add_argument("--profile-kernel", choices=["gate_up", "copy", "layer", "prefill"],
                     help="only launch this kernel 10x between read flushes (for rocprofv3 counter runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -468,6 +528,11 @@ def main() -> int:
         result["decode_step"] = decode_step(torch, data, lens, B, max(5, args.steps // 3), 2, flush_cache)
         log(f"decode step {result['decode_step']['ms_per_step']:.3f} ms, "
             f"{result['decode_step']['tokens_per_s']:.0f} tokens/s")
+    if not args.no_prefill:
+        log("timing prefill (Qwen3-8B layer over 4096 tokens, causal attention 4K/16K)")
+        result["prefill"] = prefill(torch, flush_cache)
+        log(f"prefill layer {result['prefill']['layer_T4096']['ms']:.3f} ms, "
+            f"attention 16K {result['prefill']['attention_T16384']['TFLOPs']:.0f} TFLOP/s")
     if not args.no_cpu:
         log("CPU baseline: numpy oracle of the same layer step")
         cb = cpu_baseline(torch, op, data, lens)
