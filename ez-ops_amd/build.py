@@ -18,6 +18,8 @@ PKG_ROOT = Path(__file__).resolve().parent
 CSRC = PKG_ROOT / "csrc"
 BUILD = PKG_ROOT / "_build"
 LIB = PKG_ROOT / "ezops" / "_lib" / "libezops_hip.so"
+# The same sources with wave-level timeline recording compiled in (ezops.profiling).
+PROF_LIB = PKG_ROOT / "ezops" / "_lib" / "libezops_hip_prof.so"
 ARCH = "gfx950"
 
 # Packed-fp32 VALU ops are disabled: hand-written or compiler-formed
@@ -73,11 +75,21 @@ def build(jobs: int | None = None, verbose: bool = True, extra_flags: tuple = ()
     return lib
 
 
+def build_all(jobs: int | None = None, verbose: bool = True) -> None:
+    """The production library and its profiling variant."""
+    build(jobs, verbose)
+    build(jobs, verbose, extra_flags=("-DEZ_PROFILE=1",), lib=PROF_LIB, build_dir=BUILD / "prof")
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("-j", type=int, default=None)
     ap.add_argument("-D", action="append", default=[], help="extra preprocessor definition (variant builds)")
     ap.add_argument("-o", type=Path, default=LIB, help="output library path")
+    ap.add_argument("--all", action="store_true", help="also build the profiling variant (-DEZ_PROFILE=1)")
     args = ap.parse_args()
+    if args.all:
+        build_all(args.j)
+        sys.exit(0)
     bdir = BUILD if args.o == LIB else args.o.parent / "_build"
     build(args.j, extra_flags=tuple(f"-D{d}" for d in args.D), lib=args.o, build_dir=bdir)

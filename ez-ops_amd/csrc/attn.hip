@@ -30,6 +30,7 @@
 // hand-off; an in-kernel arrival counter measured no faster on MI355X).
 #include "common.h"
 #include "internal.h"
+#include "prof.h"
 #include "status.h"
 #include "../../include/ezops_hip.h"
 
@@ -38,6 +39,8 @@
 #endif
 
 namespace ez {
+
+EZ_PROF_DEFINE(attn)
 namespace {
 
 constexpr int kTile = 32;       // positions per wave iteration
@@ -198,6 +201,7 @@ __device__ __forceinline__ int rank_to_seq(const int32_t* lens, int B, int r, in
 // PAGED: the cache is a page pool addressed through a.block_table (see KvRows).
 template <int D, int G, int W, bool LAYER, bool PAGED>
 __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int nsplit, float* opart, float* ml) {
+  EZ_PROF_WAVE(kProfAttnSplit);
   constexpr int NS = D / 32;         // MFMA k-steps per 16-position sub-tile
   constexpr int CPR = D / 8;         // 16-byte chunks per K/V row
   constexpr int RPI = kWave / CPR;   // rows covered by one wave-wide V load
@@ -481,6 +485,7 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
 template <int D>
 __global__ __launch_bounds__(D) void attn_combine_kernel(AttnArgs a, int nsplit, const float* opart,
                                                          const float* ml) {
+  EZ_PROF_WAVE(kProfAttnCombine);
   static_assert(kMaxSplits <= kWave, "one split per lane");
   const int64_t hq = blockIdx.x;
   const int lane = threadIdx.x & (kWave - 1);

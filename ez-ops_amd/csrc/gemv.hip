@@ -13,6 +13,7 @@
 // in registers) and the residual / SwiGLU epilogues of the decode layer.
 #include "common.h"
 #include "internal.h"
+#include "prof.h"
 #include "status.h"
 #include "../../include/ezops_hip.h"
 
@@ -28,6 +29,8 @@
 #endif
 
 namespace ez {
+
+EZ_PROF_DEFINE(gemv)
 namespace {
 
 constexpr int kBlock = 256;
@@ -61,6 +64,7 @@ __device__ __forceinline__ void store_out(const LinearArgs& a, int64_t m, int64_
 // flight per loop trip.
 template <int M, int R, int U, bool NORM, bool SILU>
 __global__ __launch_bounds__(kGemvBlock) void gemv_valu_kernel(LinearArgs a) {
+  EZ_PROF_WAVE(kProfGemvValu);
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t wrow = int64_t(blockIdx.x) * kGemvWaves + (threadIdx.x >> 6);
   const int64_t n0 = SILU ? wrow : wrow * R;
@@ -228,6 +232,7 @@ __device__ __forceinline__ void xfrag_fence(u32x4v_t (&x)[kMfmaSteps]) {
 
 template <int T, bool SILU, int CPW>
 __global__ __launch_bounds__(mfma_waves(T) * kWave) void linear_mfma_kernel(LinearArgs a) {
+  EZ_PROF_WAVE(kProfLinearMfma);
   constexpr int NW = mfma_waves(T);
   constexpr int XN = kMfmaSteps;         // X loads per chunk
   constexpr int DN = T * kMfmaSlices;    // DMA slices per chunk
@@ -405,6 +410,7 @@ __global__ __launch_bounds__(mfma_waves(T) * kWave) void linear_mfma_kernel(Line
 // Partial sums are reduced per wave (DPP) and across the 4 waves through LDS.
 template <int M, int RB, int CH, bool NORM, bool SILU>
 __global__ __launch_bounds__(kBlock) void gemv_rows_kernel(LinearArgs a) {
+  EZ_PROF_WAVE(kProfGemvRows);
   constexpr int NR = SILU ? 2 * RB : RB;  // weight rows per block
   constexpr int NQ = M * NR + (NORM ? M : 0);
   __shared__ float red[kWavesPerBlock][NQ];
@@ -513,6 +519,7 @@ __global__ __launch_bounds__(kBlock) void gemv_rows_kernel(LinearArgs a) {
 // Scalar fallback for K % 8 != 0 or unaligned operands: one wave per output
 // row, plain bf16 loads.
 __global__ __launch_bounds__(kBlock) void linear_scalar_kernel(LinearArgs a) {
+  EZ_PROF_WAVE(kProfLinearScalar);
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t n = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
   if (n >= a.N) return;

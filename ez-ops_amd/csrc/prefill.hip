@@ -16,10 +16,13 @@
 // is the swap between the lane halves j and j+32.
 #include "common.h"
 #include "internal.h"
+#include "prof.h"
 #include "status.h"
 #include "../../include/ezops_hip.h"
 
 namespace ez {
+
+EZ_PROF_DEFINE(prefill)
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -65,6 +68,7 @@ __device__ __forceinline__ const uint16_t* cache_row(const PrefillAttnArgs& a, c
 // keys are double-buffered in LDS (one barrier per tile).
 template <int G, bool PAGED>
 __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))) void prefill_attn_kernel(PrefillAttnArgs a, int ntq) {
+  EZ_PROF_WAVE(kProfPrefillAttn);
   constexpr int HPB = G < 4 ? G : 4;
   constexpr int NHB = G / HPB;  // head groups per kv head
   constexpr int BQ = 32 * (kPW / HPB);
@@ -237,6 +241,7 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
 // a[t][i] = silu(gu[t][i]) * gu[t][IS + i], bf16 in/out (the batched SwiGLU
 // stage between the gate/up and down GEMMs), 8 elements per thread.
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* gu, uint16_t* out, int64_t T, int64_t IS) {
+  EZ_PROF_WAVE(kProfSiluMul);
   const int64_t n8 = T * IS / 8;
   for (int64_t v = int64_t(blockIdx.x) * 256 + threadIdx.x; v < n8; v += int64_t(gridDim.x) * 256) {
     const int64_t e = v * 8, t = e / IS, i = e - t * IS;

@@ -9,15 +9,19 @@
 // the rounding.
 #include "common.h"
 #include "internal.h"
+#include "prof.h"
 #include "status.h"
 #include "../../include/ezops_hip.h"
 
 namespace ez {
+
+EZ_PROF_DEFINE(qkrope)
 namespace {
 
 constexpr int kMaxPairsPerLane = 4;  // D <= 512
 
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QkRopeArgs a) {
+  EZ_PROF_WAVE(kProfQkRope);
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t heads = a.H + a.Hkv;
   const int64_t hid = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);

@@ -7,10 +7,13 @@
 // re-reads the row.
 #include "common.h"
 #include "internal.h"
+#include "prof.h"
 #include "status.h"
 #include "../../include/ezops_hip.h"
 
 namespace ez {
+
+EZ_PROF_DEFINE(rowops)
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -22,6 +25,7 @@ template <int BS, int VPT>
 __global__ __launch_bounds__(BS) void rmsnorm_f32_reg_kernel(const float* __restrict__ X,
                                                               float* __restrict__ Out,
                                                               int64_t dim, float eps) {
+  EZ_PROF_WAVE(kProfRmsnormF32);
   __shared__ float red[BS / kWave];
   const int64_t row = blockIdx.x;
   const float4* x = reinterpret_cast<const float4*>(X + row * dim);
@@ -48,6 +52,7 @@ __global__ __launch_bounds__(BS) void rmsnorm_f32_reg_kernel(const float* __rest
 __global__ __launch_bounds__(256) void rmsnorm_f32_loop_kernel(const float* __restrict__ X,
                                                                float* __restrict__ Out,
                                                                int64_t dim, float eps) {
+  EZ_PROF_WAVE(kProfRmsnormF32);
   __shared__ float red[4];
   const float* x = X + int64_t(blockIdx.x) * dim;
   float* o = Out + int64_t(blockIdx.x) * dim;
@@ -66,6 +71,7 @@ __global__ __launch_bounds__(BS) void rmsnorm_bf16_reg_kernel(const uint16_t* __
                                                                const uint16_t* __restrict__ W,
                                                                uint16_t* __restrict__ Out,
                                                                int64_t dim, float eps) {
+  EZ_PROF_WAVE(kProfRmsnormBf16);
   __shared__ float red[BS / kWave];
   const int64_t row = blockIdx.x;
   const uint4* x = reinterpret_cast<const uint4*>(X + row * dim);
@@ -114,6 +120,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bf16_loop_kernel(const uint16_t* 
                                                                 const uint16_t* __restrict__ W,
                                                                 uint16_t* __restrict__ Out,
                                                                 int64_t dim, float eps) {
+  EZ_PROF_WAVE(kProfRmsnormBf16);
   __shared__ float red[4];
   const uint16_t* x = X + int64_t(blockIdx.x) * dim;
   uint16_t* o = Out + int64_t(blockIdx.x) * dim;
@@ -132,6 +139,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bf16_loop_kernel(const uint16_t* 
 template <int BS, int VPT>
 __global__ __launch_bounds__(BS) void softmax_reg_kernel(const float* __restrict__ X,
                                                           float* __restrict__ Out, int64_t dim) {
+  EZ_PROF_WAVE(kProfSoftmax);
   __shared__ float red[BS / kWave];
   const int64_t row = blockIdx.x;
   const float4* x = reinterpret_cast<const float4*>(X + row * dim);
@@ -168,6 +176,7 @@ __global__ __launch_bounds__(BS) void softmax_reg_kernel(const float* __restrict
 
 __global__ __launch_bounds__(1024) void softmax_loop_kernel(const float* __restrict__ X,
                                                             float* __restrict__ Out, int64_t dim) {
+  EZ_PROF_WAVE(kProfSoftmax);
   __shared__ float red[16];
   const float* x = X + int64_t(blockIdx.x) * dim;
   float* o = Out + int64_t(blockIdx.x) * dim;
@@ -200,6 +209,7 @@ int64_t sum_blocks(int64_t n) {
 __global__ __launch_bounds__(kSumBlock) void sum_kernel(const float* __restrict__ A, int64_t n,
                                                         bool vec, float* __restrict__ partial,
                                                         int* counter, float* __restrict__ Out) {
+  EZ_PROF_WAVE(kProfSum);
   __shared__ float red[kSumBlock / kWave];
   const int64_t G = gridDim.x;
   const int64_t stride = G * kSumBlock;

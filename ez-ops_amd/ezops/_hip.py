@@ -69,29 +69,36 @@ SIGNATURES: dict[str, tuple] = {
     "ezops_qwen3_decode_step_bf16": (_i32, [C.POINTER(Qwen3LayerParams), _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p,
                                             _sz, _p]),
     "ezops_hbm_probe": (_i32, [_i32, _p, _p, _p, _i64, _f32, _p]),
+    "ezops_profile_read": (_i64, [_p, _i64]),
+    "ezops_profile_reset": (_i32, []),
     "ezops_mfma_probe": (_i32, [_i32, _p, _i64, _i64, _p]),
 }
 
 _lib = None
 
 
+def load(path: Path) -> C.CDLL:
+    """Load a build of the library at ``path`` and bind every entry point."""
+    if not Path(path).exists():
+        raise RuntimeError(
+            f"{Path(path).name} not found at {path}; build it with "
+            "`python ez-ops_amd/build.py --all` (hipcc, gfx950)"
+        )
+    l = C.CDLL(str(path))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(l, name)
+        fn.restype = res
+        fn.argtypes = args
+    if l.ezops_hip_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{path}: ABI version {l.ezops_hip_abi_version()} != {ABI_VERSION}")
+    return l
+
+
 def lib() -> C.CDLL:
     """Load (once) and return the HIP library; raise if it is absent."""
     global _lib
     if _lib is None:
-        if not LIB_PATH.exists():
-            raise RuntimeError(
-                f"libezops_hip.so not found at {LIB_PATH}; build it with "
-                "`python ez-ops_amd/build.py` (hipcc, gfx950)"
-            )
-        l = C.CDLL(str(LIB_PATH))
-        for name, (res, args) in SIGNATURES.items():
-            fn = getattr(l, name)
-            fn.restype = res
-            fn.argtypes = args
-        if l.ezops_hip_abi_version() != ABI_VERSION:
-            raise RuntimeError(f"{LIB_PATH}: ABI version {l.ezops_hip_abi_version()} != {ABI_VERSION}")
-        _lib = l
+        _lib = load(LIB_PATH)
     return _lib
 
 

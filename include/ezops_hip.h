@@ -34,6 +34,7 @@ extern "C" {
 
 #define EZOPS_HIP_ABI_VERSION 2
 #define EZOPS_EINVAL (-22)
+#define EZOPS_ENOSYS (-38) /* feature not compiled into this build */
 
 int ezops_hip_abi_version(void);
 const char* ezops_hip_last_error(void);
@@ -272,6 +273,26 @@ size_t ezops_gemm_workspace_size(void);
 int ezops_gemm_bf16(const void* X, int64_t ldx, const void* W, void* Y, int64_t ldy, const void* R,
                     int64_t M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
                     hipStream_t stream);
+
+/* Wave-level kernel timelines (a library built with -DEZ_PROFILE=1; the
+ * production build returns EZOPS_ENOSYS).  Every wave of the instrumented
+ * kernels (GEMV/GEMM, decode and prefill attention, combine, norms, softmax,
+ * sum, qk-norm/RoPE, SwiGLU) appends one 32-byte record when it ends:
+ *   uint64 t0, t1   s_memrealtime ticks (100 MHz) at wave begin / end
+ *   uint32 hw_id    HW_ID register (wave slot 3:0, SIMD 5:4, CU 11:8, SH 12, SE 15:13)
+ *   uint32 xcc_id   XCC_ID register (XCD in bits 3:0)
+ *   uint16 kernel   kernel id (1 gemv_rows, 2 gemv_valu, 3 linear_scalar, 4 linear_mfma,
+ *                   5 attn_split, 6 attn_combine, 7 prefill_attn, 8 silu_mul,
+ *                   9 qk_norm_rope, 10 rmsnorm_f32, 11 rmsnorm_bf16, 12 softmax, 13 sum)
+ *   uint16 wave     wave index in its block;  uint32 block  blockIdx.x
+ * ezops_profile_reset clears the buffers; ezops_profile_read copies up to
+ * `capacity` records to host memory and returns how many (both synchronise
+ * the device).  Up to 2^18 records per kernel source file are kept.
+ * Replaces: the reference's advertised SM-level profiling with Perfetto
+ * export (README.md:13), which its tree does not implement (its profiling is
+ * scripts/ncu_profile.py, an Nsight Compute wrapper). */
+int64_t ezops_profile_read(void* records, int64_t capacity);
+int ezops_profile_reset(void);
 
 /* STREAM-style HBM probes used to measure the chip's bandwidth peak
  * (replaces benchmarks/hardware/memory/hbm_saturation.cu:49-90):
