@@ -12,6 +12,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <vector>
+
 #ifndef EZ_PROFILE
 #define EZ_PROFILE 0
 #endif
@@ -32,7 +34,12 @@ enum ProfKernel : uint16_t {
   kProfPrefillAttn, kProfSiluMul, kProfQkRope, kProfRmsnormF32, kProfRmsnormBf16, kProfSoftmax, kProfSum,
 };
 
-constexpr uint32_t kProfCap = 1u << 18;  // records per translation unit (8 MiB)
+// Records are appended per CU (region = XCC, SE, SH, CU from the hardware
+// registers), each region with its own counter, so no counter is shared by
+// more than the waves of one CU.
+constexpr uint32_t kProfRegions = 8 * 8 * 2 * 16;
+constexpr uint32_t kProfRegionCap = 512;
+constexpr uint32_t kProfCap = kProfRegions * kProfRegionCap;  // records per translation unit (32 MiB)
 
 // Host side: every translation unit with a buffer registers its reader.
 using ProfRead = int (*)(WaveRecord* host, size_t cap, size_t* n);
@@ -51,18 +58,18 @@ struct ProfScope {
   __device__ ~ProfScope() {
     const unsigned long long t1 = __builtin_amdgcn_s_memrealtime();
     if ((threadIdx.x & 63) == 0) {
-      const unsigned long long i = atomicAdd(count, 1ull);  // vector atomic from one lane
-      if (i < kProfCap) {
-        WaveRecord r;
-        r.t0 = t0;
-        r.t1 = t1;
-        r.hw_id = __builtin_amdgcn_s_getreg((31 << 11) | 4);   // HW_ID, 32 bits
-        r.xcc_id = __builtin_amdgcn_s_getreg((15 << 11) | 20); // XCC_ID, 16 bits
-        r.kernel = kid;
-        r.wave = uint16_t(threadIdx.x >> 6);
-        r.block = blockIdx.x;
-        buf[i] = r;
-      }
+      WaveRecord r;
+      r.t0 = t0;
+      r.t1 = t1;
+      r.hw_id = __builtin_amdgcn_s_getreg((31 << 11) | 4);   // HW_ID, 32 bits
+      r.xcc_id = __builtin_amdgcn_s_getreg((15 << 11) | 20); // XCC_ID, 16 bits
+      r.kernel = kid;
+      r.wave = uint16_t(threadIdx.x >> 6);
+      r.block = blockIdx.x;
+      const uint32_t region = ((((r.xcc_id & 7u) * 8u + ((r.hw_id >> 13) & 7u)) * 2u + ((r.hw_id >> 12) & 1u)) * 16u) +
+                              ((r.hw_id >> 8) & 15u);
+      const unsigned long long i = atomicAdd(count + region, 1ull);  // vector atomic from one lane
+      if (i < kProfRegionCap) buf[region * kProfRegionCap + i] = r;
     }
   }
 };
@@ -71,28 +78,35 @@ struct ProfScope {
 // separate code objects) plus its host reader, registered at load time.
 #define EZ_PROF_DEFINE(tu)                                                                               \
   __device__ ::ez::WaveRecord ez_prof_buf_##tu[::ez::kProfCap];                                          \
-  __device__ unsigned long long ez_prof_n_##tu;                                                          \
+  __device__ unsigned long long ez_prof_n_##tu[::ez::kProfRegions];                                      \
   namespace {                                                                                            \
   __device__ __forceinline__ ::ez::WaveRecord* ez_prof_buf() { return ez_prof_buf_##tu; }                \
-  __device__ __forceinline__ unsigned long long* ez_prof_count() { return &ez_prof_n_##tu; }             \
+  __device__ __forceinline__ unsigned long long* ez_prof_count() { return ez_prof_n_##tu; }              \
   int ez_prof_read_##tu(::ez::WaveRecord* host, size_t cap, size_t* n) {                                 \
-    unsigned long long cnt = 0;                                                                          \
-    if (hipMemcpyFromSymbol(&cnt, HIP_SYMBOL(ez_prof_n_##tu), sizeof(cnt), 0, hipMemcpyDeviceToHost) !=  \
-        hipSuccess)                                                                                      \
-      return -1;                                                                                         \
-    size_t k = cnt < ::ez::kProfCap ? size_t(cnt) : size_t(::ez::kProfCap);                              \
-    k = k < cap ? k : cap;                                                                               \
-    *n = k;                                                                                              \
-    if (k && host &&                                                                                     \
-        hipMemcpyFromSymbol(host, HIP_SYMBOL(ez_prof_buf_##tu), k * sizeof(::ez::WaveRecord), 0,         \
+    std::vector<unsigned long long> cnt(::ez::kProfRegions);                                             \
+    std::vector<::ez::WaveRecord> all(::ez::kProfCap);                                                   \
+    if (hipMemcpyFromSymbol(cnt.data(), HIP_SYMBOL(ez_prof_n_##tu), cnt.size() * sizeof(cnt[0]), 0,      \
+                            hipMemcpyDeviceToHost) != hipSuccess ||                                      \
+        hipMemcpyFromSymbol(all.data(), HIP_SYMBOL(ez_prof_buf_##tu), all.size() * sizeof(all[0]), 0,    \
                             hipMemcpyDeviceToHost) != hipSuccess)                                        \
       return -1;                                                                                         \
-    return cnt > ::ez::kProfCap ? 1 : 0;                                                                 \
+    size_t k = 0;                                                                                        \
+    bool lost = false;                                                                                   \
+    for (uint32_t g = 0; g < ::ez::kProfRegions; ++g) {                                                  \
+      const size_t m = cnt[g] < ::ez::kProfRegionCap ? size_t(cnt[g]) : size_t(::ez::kProfRegionCap);    \
+      lost |= cnt[g] > ::ez::kProfRegionCap;                                                             \
+      for (size_t i = 0; i < m && k < cap; ++i) {                                                        \
+        if (host) host[k] = all[size_t(g) * ::ez::kProfRegionCap + i];                                   \
+        ++k;                                                                                             \
+      }                                                                                                  \
+    }                                                                                                    \
+    *n = k;                                                                                              \
+    return lost ? 1 : 0;                                                                                 \
   }                                                                                                      \
   int ez_prof_reset_##tu() {                                                                             \
-    const unsigned long long z = 0;                                                                      \
-    return hipMemcpyToSymbol(HIP_SYMBOL(ez_prof_n_##tu), &z, sizeof(z), 0, hipMemcpyHostToDevice) ==     \
-                   hipSuccess                                                                            \
+    const std::vector<unsigned long long> z(::ez::kProfRegions, 0ull);                                   \
+    return hipMemcpyToSymbol(HIP_SYMBOL(ez_prof_n_##tu), z.data(), z.size() * sizeof(z[0]), 0,           \
+                             hipMemcpyHostToDevice) == hipSuccess                                        \
                ? 0                                                                                       \
                : -1;                                                                                     \
   }                                                                                                      \

@@ -287,7 +287,7 @@ int ezops_gemm_bf16(const void* X, int64_t ldx, const void* W, void* Y, int64_t 
  *   uint16 wave     wave index in its block;  uint32 block  blockIdx.x
  * ezops_profile_reset clears the buffers; ezops_profile_read copies up to
  * `capacity` records to host memory and returns how many (both synchronise
- * the device).  Up to 2^18 records per kernel source file are kept.
+ * the device).  Up to 512 records per CU and kernel source file are kept.
  * Replaces: the reference's advertised SM-level profiling with Perfetto
  * export (README.md:13), which its tree does not implement (its profiling is
  * scripts/ncu_profile.py, an Nsight Compute wrapper). */
