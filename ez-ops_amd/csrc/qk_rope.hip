@@ -20,6 +20,33 @@ namespace {
 
 constexpr int kMaxPairsPerLane = 4;  // D <= 512
 
+// Sequence and cache position of row b (a decode batch row or a prefill token).
+__device__ __forceinline__ void row_position(const QkRopeArgs& a, int64_t b, int64_t& seq, int64_t& pos) {
+  seq = b;
+  if (a.cu) {  // prefill row: find its sequence (binary search over cu)
+    int64_t lo = 0, hi = a.nseq - 1;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi + 1) >> 1;
+      if (a.cu[mid] <= b) lo = mid; else hi = mid - 1;
+    }
+    seq = lo;
+    pos = (a.past ? int64_t(a.past[seq]) : 0) + b - a.cu[seq];
+  } else {
+    pos = (a.positions ? int64_t(a.positions[b]) : a.position) + a.pos_offset;
+  }
+}
+
+// Element offset of cache row (seq, kv head, pos): contiguous or paged.
+__device__ __forceinline__ int64_t cache_offset(const QkRopeArgs& a, int64_t seq, int64_t kvh, int64_t pos) {
+  if (a.block_table) {
+    const int sh = __builtin_ctz(unsigned(a.page_size));
+    const int64_t pg = pos >> sh;
+    const uint32_t id = min(uint32_t(a.block_table[seq * a.bt_stride + pg]), uint32_t(a.num_pages - 1));
+    return ((int64_t(id) * a.Hkv + kvh) * a.page_size + (pos - (pg << sh))) * a.D;
+  }
+  return ((seq * a.Hkv + kvh) * a.S + pos) * a.D;
+}
+
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QkRopeArgs a) {
   EZ_PROF_WAVE(kProfQkRope);
   const int lane = threadIdx.x & (kWave - 1);
@@ -31,18 +58,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QkRopeArgs a) {
   const int64_t kvh = h - a.H;
   const uint16_t* src = is_q ? a.q + b * a.q_bs + h * a.D : a.k + b * a.k_bs + kvh * a.D;
   const uint16_t* w = is_q ? a.qw : a.kw;
-  int64_t seq = b, pos;
-  if (a.cu) {  // prefill row: find its sequence (wave-uniform binary search)
-    int64_t lo = 0, hi = a.nseq - 1;
-    while (lo < hi) {
-      const int64_t mid = (lo + hi + 1) >> 1;
-      if (a.cu[mid] <= b) lo = mid; else hi = mid - 1;
-    }
-    seq = lo;
-    pos = (a.past ? int64_t(a.past[seq]) : 0) + b - a.cu[seq];
-  } else {
-    pos = (a.positions ? int64_t(a.positions[b]) : a.position) + a.pos_offset;
-  }
+  int64_t seq, pos;
+  row_position(a, b, seq, pos);
   const int64_t half = a.D / 2;
   // Positions can come from device memory (per-sequence arrays), so they are
   // range-checked here: an out-of-range position writes nothing.
@@ -61,18 +78,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QkRopeArgs a) {
 
   const uint16_t* crow = a.cos ? a.cos + pos * a.D : nullptr;
   const uint16_t* srow = a.sin ? a.sin + pos * a.D : nullptr;
-  // cache row offset (elements) of (seq, kvh, pos)
-  int64_t crow_off = 0;
-  if (!is_q) {
-    if (a.block_table) {
-      const int sh = __builtin_ctz(unsigned(a.page_size));
-      const int64_t pg = pos >> sh;
-      const uint32_t id = min(uint32_t(a.block_table[seq * a.bt_stride + pg]), uint32_t(a.num_pages - 1));
-      crow_off = ((int64_t(id) * a.Hkv + kvh) * a.page_size + (pos - (pg << sh))) * a.D;
-    } else {
-      crow_off = ((seq * a.Hkv + kvh) * a.S + pos) * a.D;
-    }
-  }
+  const int64_t crow_off = is_q ? 0 : cache_offset(a, seq, kvh, pos);
   uint16_t* dst = is_q ? a.q_out + (b * a.H + h) * a.D : a.Kc + crow_off;
   uint16_t* kdst = (!is_q && a.k_out) ? a.k_out + (b * a.Hkv + kvh) * a.D : nullptr;
 #pragma unroll
@@ -104,6 +110,76 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QkRopeArgs a) {
   }
 }
 
+// D in {64, 128, 256}: D/8 lanes per head, each lane holding 8 consecutive
+// elements (16-byte loads and stores), 64/(D/8) heads per wave.  RoPE pairs
+// (i, i + D/2) sit in lanes l and l ^ (D/16) of the head's lane group, so the
+// partner half arrives by one lane exchange.  Same fp32 operations and
+// rounding as the kernel above.
+template <int D>
+__global__ __launch_bounds__(256) void qk_norm_rope_vec_kernel(QkRopeArgs a) {
+  EZ_PROF_WAVE(kProfQkRope);
+  constexpr int LPH = D / 8;
+  constexpr int HPW = kWave / LPH;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int l = lane % LPH;
+  const int64_t heads = a.H + a.Hkv;
+  const int64_t hid = (int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6)) * HPW + lane / LPH;
+  const bool live = hid < a.B * heads;
+  const int64_t hc = live ? hid : 0;  // dead lanes still join the exchanges, on a valid row
+  const int64_t b = hc / heads, h = hc % heads;
+  const bool is_q = h < a.H;
+  const int64_t kvh = h - a.H;
+  int64_t seq, pos;
+  row_position(a, b, seq, pos);
+  const bool ok = live && pos >= 0 && pos < a.S;
+  const int64_t posc = ok ? pos : 0;
+  const uint16_t* src = (is_q ? a.q + b * a.q_bs + h * D : a.k + b * a.k_bs + kvh * D) + 8 * l;
+  const uint16_t* w = is_q ? a.qw : a.kw;
+
+  float x[8];
+  unpack8(*reinterpret_cast<const uint4*>(src), x);
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+#pragma unroll
+  for (int o = LPH / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, kWave);
+  const float r = rsqrtf(ss / float(D) + a.eps);
+  float y[8], wf[8];
+  if (w) unpack8(*reinterpret_cast<const uint4*>(w + 8 * l), wf);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    y[e] = __fmul_rn(x[e], r);
+    if (w) y[e] = __fmul_rn(y[e], wf[e]);
+  }
+  float o[8];
+  if (a.cos) {
+    float c[8], sn[8], yp[8];
+    unpack8(*reinterpret_cast<const uint4*>(a.cos + posc * D + 8 * l), c);
+    unpack8(*reinterpret_cast<const uint4*>(a.sin + posc * D + 8 * l), sn);
+    const bool first = l < LPH / 2;  // this lane holds y1 (i < D/2), its partner y2
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      yp[e] = __shfl_xor(y[e], LPH / 2, kWave);
+      o[e] = __fadd_rn(__fmul_rn(y[e], c[e]), __fmul_rn(first ? -yp[e] : yp[e], sn[e]));
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = y[e];
+  }
+  if (!ok) return;
+  const uint4 packed = make_uint4(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]), pack_bf2(o[4], o[5]), pack_bf2(o[6], o[7]));
+  if (is_q) {
+    *reinterpret_cast<uint4*>(a.q_out + (b * a.H + h) * D + 8 * l) = packed;
+  } else {
+    const int64_t off = cache_offset(a, seq, kvh, pos) + 8 * l;
+    *reinterpret_cast<uint4*>(a.Kc + off) = packed;
+    if (a.k_out) *reinterpret_cast<uint4*>(a.k_out + (b * a.Hkv + kvh) * D + 8 * l) = packed;
+    *reinterpret_cast<uint4*>(a.Vc + off) = *reinterpret_cast<const uint4*>(a.v + b * a.v_bs + kvh * D + 8 * l);
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 }  // namespace
 
 int launch_qk_norm_rope(const QkRopeArgs& a, hipStream_t s) {
@@ -116,8 +192,21 @@ int launch_qk_norm_rope(const QkRopeArgs& a, hipStream_t s) {
   EZ_REQUIRE(!a.block_table || (a.page_size >= 1 && (a.page_size & (a.page_size - 1)) == 0 && a.num_pages >= 1 &&
                                 a.S == a.bt_stride * a.page_size),
              "qk_norm_rope: paged cache needs a power-of-two page_size and S = max_pages * page_size");
-  const int64_t waves = a.B * (a.H + a.Hkv);
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(unsigned((waves + 3) / 4)), dim3(256), 0, s, a);
+  const int64_t heads = a.B * (a.H + a.Hkv);
+  const bool vec = (a.D == 64 || a.D == 128 || a.D == 256) && a.q_bs % 8 == 0 && a.k_bs % 8 == 0 &&
+                   a.v_bs % 8 == 0 && aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.Kc) &&
+                   aligned16(a.Vc) && aligned16(a.q_out) && (!a.k_out || aligned16(a.k_out)) &&
+                   (!a.qw || aligned16(a.qw)) && (!a.kw || aligned16(a.kw)) && (!a.cos || aligned16(a.cos)) &&
+                   (!a.sin || aligned16(a.sin));
+  if (vec) {
+    const int64_t hpw = kWave / (a.D / 8);
+    const unsigned blocks = unsigned((heads + 4 * hpw - 1) / (4 * hpw));
+    if (a.D == 64) hipLaunchKernelGGL(qk_norm_rope_vec_kernel<64>, dim3(blocks), dim3(256), 0, s, a);
+    else if (a.D == 128) hipLaunchKernelGGL(qk_norm_rope_vec_kernel<128>, dim3(blocks), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(qk_norm_rope_vec_kernel<256>, dim3(blocks), dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(unsigned((heads + 3) / 4)), dim3(256), 0, s, a);
+  }
   return launch_status("qk_norm_rope");
 }
 

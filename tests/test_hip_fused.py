@@ -52,6 +52,22 @@ def test_fused_qk_norm_rope(batch, max_seq_len, position, num_kv_heads):
         assert torch.equal(Vc[b][:, mask], V0[b][:, mask])
 
 
+@pytest.mark.parametrize("head_dim,num_kv_heads", [(32, 4), (64, 2), (256, 8)])
+def test_fused_qk_norm_rope_head_dims(head_dim, num_kv_heads):
+    """head_dim 64/256 take the 16-byte-lane kernel, 32 the one-pair-per-lane one."""
+    torch.manual_seed(3)
+    op = FusedQkNormRopeOp(3, num_heads=16, head_dim=head_dim, max_seq_len=300, position=[0, 299, 17],
+                           num_kv_heads=num_kv_heads, backend="hip")
+    data = op.gen_data()
+    K0, V0 = data[7].clone(), data[8].clone()
+    q_out, k_out = op(*data)
+    rq, rk, rK, rV = oracle.qk_norm_rope(*[n(x) for x in data[:7]], n(K0), n(V0), np.array([0, 299, 17]))
+    np.testing.assert_allclose(n(q_out), rq, **BF_TOL)
+    np.testing.assert_allclose(n(k_out), rk, **BF_TOL)
+    np.testing.assert_allclose(n(data[7]), rK, **BF_TOL)
+    assert torch.equal(data[8].cpu().float(), torch.from_numpy(rV))
+
+
 @pytest.mark.parametrize("batch,shape", [(1, QWEN3_VL_2B), (1, QWEN3_0_6B), (2, QWEN3_VL_2B), (4, QWEN3_VL_2B),
                                          (1, QWEN3_8B), (16, QWEN3_8B), (7, QWEN3_0_6B)])
 def test_fused_o_proj_ffn(batch, shape):
