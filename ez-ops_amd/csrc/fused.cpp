@@ -335,7 +335,7 @@ extern "C" int ezops_qwen3_prefill_bf16(const ezops_qwen3_layer* p, int64_t T, c
   a.Out = w.att; a.o_rs = QR;
   a.cu = cu_seqlens; a.past = p->kv_lens;
   a.block_table = block_table; a.bt_stride = r.bt_stride; a.page_size = r.page_size; a.num_pages = num_pages;
-  a.B = p->B; a.H = p->H; a.Hkv = p->Hkv; a.S = p->S; a.D = p->D; a.max_q = max_q_len;
+  a.B = p->B; a.T = T; a.H = p->H; a.Hkv = p->Hkv; a.S = p->S; a.D = p->D; a.max_q = max_q_len;
   a.scale = 0.f;
   rc = launch_prefill_attn(a, s);
   if (!rc) rc = gemm_bf16(w.att, QR, W(p->Wo), w.h, HS, hidden, T, HS, QR, w.gemm_ws, kGemmWorkspace, s);

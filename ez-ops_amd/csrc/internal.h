@@ -105,7 +105,7 @@ struct PrefillAttnArgs {
   uint16_t* Out; int64_t o_rs;
   const int32_t* cu; const int32_t* past;  // [B + 1], [B] (NULL = 0)
   const int32_t* block_table; int64_t bt_stride; int page_size; int64_t num_pages;
-  int64_t B, H, Hkv, S, D, max_q;
+  int64_t B, T, H, Hkv, S, D, max_q;  // T: rows of Q / Out
   float scale;
 };
 int launch_prefill_attn(const PrefillAttnArgs& a, hipStream_t s);

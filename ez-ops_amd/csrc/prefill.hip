@@ -81,9 +81,11 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
   const int hb = rem % NHB;
   rem /= NHB;
   const int b = rem / int(a.Hkv), kvh = rem % int(a.Hkv);
-  const int64_t q0 = a.cu[b];
-  const int64_t qlen0 = int64_t(a.cu[b + 1]) - q0;
-  const int64_t past = a.past ? int64_t(a.past[b]) : 0;
+  // Offsets and lengths come from device memory: clamp them into Q/Out's T
+  // rows and the cache capacity so that no access leaves the buffers.
+  const int64_t q0 = min(max(int64_t(a.cu[b]), int64_t(0)), a.T);
+  const int64_t qlen0 = min(int64_t(a.cu[b + 1]), a.T) - q0;
+  const int64_t past = min(max(a.past ? int64_t(a.past[b]) : 0, int64_t(0)), a.S);
   // rows past the cache capacity are neither read nor written
   const int64_t qlen = min(qlen0, a.S - past);
   if (int64_t(qt) * BQ >= qlen) return;
@@ -264,7 +266,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* gu, uint1
 
 int launch_prefill_attn(const PrefillAttnArgs& a, hipStream_t s) {
   EZ_REQUIRE(a.Q && a.K && a.V && a.Out && a.cu, "prefill_attn: null pointer");
-  EZ_REQUIRE(a.B >= 1 && a.H >= 1 && a.Hkv >= 1 && a.S >= 1 && a.max_q >= 0, "prefill_attn: bad shape");
+  EZ_REQUIRE(a.B >= 1 && a.T >= 0 && a.H >= 1 && a.Hkv >= 1 && a.S >= 1 && a.max_q >= 0, "prefill_attn: bad shape");
   EZ_REQUIRE(a.D == kPD, "prefill_attn: head_dim must be %d", kPD);
   EZ_REQUIRE(a.H % a.Hkv == 0, "prefill_attn: num_heads must be divisible by num_kv_heads");
   const int64_t G = a.H / a.Hkv;
@@ -308,7 +310,7 @@ int launch_silu_mul(const uint16_t* gu, uint16_t* out, int64_t T, int64_t IS, hi
 }  // namespace ez
 
 extern "C" int ezops_prefill_attn_bf16(const void* Q, const void* K, const void* V, void* Out,
-                                       const int32_t* cu_seqlens, const int32_t* past_lens, int64_t B,
+                                       const int32_t* cu_seqlens, const int32_t* past_lens, int64_t B, int64_t T,
                                        int64_t H, int64_t Hkv, int64_t S, int64_t D, int64_t max_q_len,
                                        const int32_t* block_table, int64_t num_pages, int64_t page_size,
                                        float scale, hipStream_t stream) {
@@ -317,7 +319,7 @@ extern "C" int ezops_prefill_attn_bf16(const void* Q, const void* K, const void*
   a.K = static_cast<const uint16_t*>(K); a.V = static_cast<const uint16_t*>(V);
   a.Out = static_cast<uint16_t*>(Out); a.o_rs = H * D;
   a.cu = cu_seqlens; a.past = past_lens;
-  a.B = B; a.H = H; a.Hkv = Hkv; a.S = S; a.D = D; a.max_q = max_q_len;
+  a.B = B; a.T = T; a.H = H; a.Hkv = Hkv; a.S = S; a.D = D; a.max_q = max_q_len;
   a.block_table = block_table;
   if (block_table) {
     EZ_REQUIRE(page_size >= 1 && S % page_size == 0, "prefill_attn: S must be a multiple of page_size");

@@ -50,7 +50,7 @@ class PrefillAttnHipKernel(BaseKernel):
         cu, past = self.meta(dev)
         Out = torch.empty(self.T, self.H, self.D, dtype=bf, device=dev)
         _hip.call("ezops_prefill_attn_bf16", Q.data_ptr(), K_cache.data_ptr(), V_cache.data_ptr(), Out.data_ptr(),
-                  cu.data_ptr(), past.data_ptr(), self.B, self.H, self.Hkv, self.S, self.D,
+                  cu.data_ptr(), past.data_ptr(), self.B, self.T, self.H, self.Hkv, self.S, self.D,
                   max(self.q_lens, default=0), _hip.ptr(block_table), self.num_pages or 0, self.page_size or 0, 0.0,
                   _hip.stream(dev))
         return Out

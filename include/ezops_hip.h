@@ -143,12 +143,14 @@ int ezops_paged_attn_decode_bf16(const void* Q, const void* K_pages, const void*
  * [num_pages, Hkv, page_size, D] with block_table [B, S / page_size] when
  * block_table != NULL.  max_q_len: host bound on the per-sequence token
  * counts (grid size).  D = 128; H / Hkv in {1, 2, 4, 8}; scale <= 0 selects
- * 1/sqrt(D).  Rows at or beyond S are skipped.
+ * 1/sqrt(D).  T: rows of Q / Out.  Offsets and lengths are clamped into
+ * [0, T] rows and [0, S] cache rows on the device; rows at or beyond S are
+ * skipped (left unwritten).
  * No counterpart in the reference (decode only, ezops/ops/attn_decode.py:9-67):
  * the step before the decode path, writing the cache it reads. */
 int ezops_prefill_attn_bf16(const void* Q, const void* K, const void* V, void* Out,
-                            const int32_t* cu_seqlens, const int32_t* past_lens, int64_t B, int64_t H,
-                            int64_t Hkv, int64_t S, int64_t D, int64_t max_q_len,
+                            const int32_t* cu_seqlens, const int32_t* past_lens, int64_t B, int64_t T,
+                            int64_t H, int64_t Hkv, int64_t S, int64_t D, int64_t max_q_len,
                             const int32_t* block_table, int64_t num_pages, int64_t page_size,
                             float scale, hipStream_t stream);
 

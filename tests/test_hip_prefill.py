@@ -126,3 +126,23 @@ def test_qwen3_prefill_paged_equals_contiguous_then_decode():
     ref, _, _ = oracle.qwen3_layer(n(hid), K_before, V_before, *npw[:4], 32, 8, 128, kv_lens=lens, in_norm_w=npw[4],
                                    q_norm_w=npw[5], k_norm_w=npw[6], post_norm_w=npw[7], cos=npw[8], sin=npw[9])
     assert dop.check(dout, torch.from_numpy(ref).cuda())
+
+
+def test_prefill_attn_clamps_device_lengths():
+    """cu_seqlens / past_lens live in device memory and are clamped there: a
+    negative past length acts as 0 and offsets past T end the sequence."""
+    torch.manual_seed(12)
+    op = PrefillAttnOp(2, 32, 8, 128, 512, [100, 50], [0, 0], backend="hip")
+    Q, K, V = op.gen_data()
+    ref = op(Q, K, V)
+    cu = torch.tensor([0, 100, 150], dtype=torch.int32, device="cuda")
+    past = torch.tensor([-3, 0], dtype=torch.int32, device="cuda")
+    out = torch.zeros_like(ref)
+    _hip.call("ezops_prefill_attn_bf16", Q.data_ptr(), K.data_ptr(), V.data_ptr(), out.data_ptr(), cu.data_ptr(),
+              past.data_ptr(), 2, 150, 32, 8, 512, 128, 100, None, 0, 0, 0.0, _hip.stream())
+    assert torch.equal(out, ref)
+    cu_over = torch.tensor([0, 100, 4000], dtype=torch.int32, device="cuda")  # second sequence runs past T = 150
+    out2 = torch.zeros_like(ref)
+    _hip.call("ezops_prefill_attn_bf16", Q.data_ptr(), K.data_ptr(), V.data_ptr(), out2.data_ptr(),
+              cu_over.data_ptr(), None, 2, 150, 32, 8, 512, 128, 100, None, 0, 0, 0.0, _hip.stream())
+    assert torch.equal(out2, ref)
