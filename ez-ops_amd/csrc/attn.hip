@@ -510,17 +510,6 @@ __global__ __launch_bounds__(D) void attn_combine_kernel(AttnArgs a, int nsplit,
   a.Out[out_index(a, hq, d)] = f2bf(acc);
 }
 
-int num_cus() {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-      cus = 256;
-  }
-  return cus;
-}
-
 struct SplitPlan {
   int waves;
   int nsplit;

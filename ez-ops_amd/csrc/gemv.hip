@@ -187,7 +187,6 @@ constexpr int kMfmaKC = 256;                     // K elements per chunk
 constexpr int kMfmaSteps = kMfmaKC / 32;         // MFMA k-steps per chunk
 constexpr int kMfmaSlices = 16 * kMfmaKC / 512;  // 1 KiB DMA slices per 16-row tile and chunk
 
-__host__ __device__ constexpr int mfma_waves(int T) { return T == 1 ? 8 : 4; }
 
 // s_waitcnt with vmcnt = N and the other counters unconstrained (gfx9 encoding).
 template <int N>
@@ -230,10 +229,9 @@ __device__ __forceinline__ void xfrag_fence(u32x4v_t (&x)[kMfmaSteps]) {
                     "+v"(x[7]));
 }
 
-template <int T, bool SILU, int CPW>
-__global__ __launch_bounds__(mfma_waves(T) * kWave) void linear_mfma_kernel(LinearArgs a) {
+template <int T, bool SILU, int CPW, int NW>
+__global__ __launch_bounds__(NW * kWave) void linear_mfma_kernel(LinearArgs a) {
   EZ_PROF_WAVE(kProfLinearMfma);
-  constexpr int NW = mfma_waves(T);
   constexpr int XN = kMfmaSteps;         // X loads per chunk
   constexpr int DN = T * kMfmaSlices;    // DMA slices per chunk
   // One array per ring stage: distinct LDS objects.
@@ -604,14 +602,13 @@ void launch_valu_m(const LinearArgs& a, hipStream_t s) {
   }
 }
 
-template <bool SILU>
-void launch_mfma(const LinearArgs& a, hipStream_t s) {
+template <bool SILU, int NW>
+void launch_mfma_nw(const LinearArgs& a, hipStream_t s) {
   constexpr int T = SILU ? 2 : 1;
-  constexpr int NW = mfma_waves(T);
   const dim3 grid(unsigned((a.N + 15) / 16), unsigned((a.M + 15) / 16)), block(NW * kWave);
   const int64_t nchunks = (a.K + kMfmaKC - 1) / kMfmaKC;
   const int64_t cpw = nchunks % NW == 0 ? nchunks / NW : 0;
-#define EZ_MFMA_LAUNCH(C) hipLaunchKernelGGL((linear_mfma_kernel<T, SILU, C>), grid, block, 0, s, a)
+#define EZ_MFMA_LAUNCH(C) hipLaunchKernelGGL((linear_mfma_kernel<T, SILU, C, NW>), grid, block, 0, s, a)
   switch (cpw) {
     case 1: EZ_MFMA_LAUNCH(1); break;
     case 2: EZ_MFMA_LAUNCH(2); break;
@@ -620,6 +617,21 @@ void launch_mfma(const LinearArgs& a, hipStream_t s) {
     default: EZ_MFMA_LAUNCH(0); break;
   }
 #undef EZ_MFMA_LAUNCH
+}
+
+// Blocks of 16 weight rows (T=2: 16 gate + 16 up).  An 8-wave T=1 block
+// holds 136 KB of LDS, one per CU; when the tiles outnumber the CUs but not
+// twice over (QKV at 6144 rows: 384 tiles), 4-wave blocks (68 KB) share a CU
+// two by two so every tile runs in the first round instead of 1.5 rounds.
+template <bool SILU>
+void launch_mfma(const LinearArgs& a, hipStream_t s) {
+  if constexpr (SILU) {
+    launch_mfma_nw<true, 4>(a, s);
+  } else {
+    const int64_t tiles = ((a.N + 15) / 16) * ((a.M + 15) / 16), cus = num_cus();
+    if (tiles > cus && tiles <= 2 * cus) launch_mfma_nw<false, 4>(a, s);
+    else launch_mfma_nw<false, 8>(a, s);
+  }
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }

@@ -305,16 +305,6 @@ __global__ __launch_bounds__(256) void probe_stream_kernel(f32x4v_t* __restrict_
   }
 }
 
-int num_cus() {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-      cus = 256;
-  }
-  return cus;
-}
-
 template <int BS>
 void launch_rms_f32(const float* X, float* O, int64_t rows, int64_t dim, float eps, hipStream_t s) {
   const int64_t vpt = (dim / 4 + BS - 1) / BS;

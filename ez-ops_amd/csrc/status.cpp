@@ -6,6 +6,19 @@
 #include "../../include/ezops_hip.h"
 
 namespace ez {
+
+int num_cus() {
+  static int cus = 0;  // the first device queried (one GPU per process)
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cus = n;
+  }
+  return cus;
+}
+
 namespace {
 thread_local char g_err[512] = "";
 }

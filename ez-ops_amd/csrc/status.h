@@ -10,6 +10,8 @@ namespace ez {
 int set_error(int code, const char* fmt, ...);
 // Map the launch status of the kernels just enqueued to a return code.
 int launch_status(const char* what);
+// Compute units of the current device (256 on MI355X).
+int num_cus();
 }  // namespace ez
 
 #define EZ_REQUIRE(cond, ...)                                      \
