@@ -229,7 +229,10 @@ __device__ __forceinline__ void xfrag_fence(u32x4v_t (&x)[kMfmaSteps]) {
                     "+v"(x[7]));
 }
 
-template <int T, bool SILU, int CPW, int NW>
+// TPB > 1 (with CPW > 0): the block walks tiles blockIdx.x + k * gridDim.x,
+// k < TPB, as one stream of chunks, so the ring's DMAs for a tile's first
+// chunks are in flight during the previous tile's epilogue.
+template <int T, bool SILU, int CPW, int NW, int TPB>
 __global__ __launch_bounds__(NW * kWave) void linear_mfma_kernel(LinearArgs a) {
   EZ_PROF_WAVE(kProfLinearMfma);
   constexpr int XN = kMfmaSteps;         // X loads per chunk
@@ -243,20 +246,23 @@ __global__ __launch_bounds__(NW * kWave) void linear_mfma_kernel(LinearArgs a) {
   const int i = lane & 15, g = lane >> 4;
   const int64_t m0 = int64_t(blockIdx.y) * 16;
   const int64_t m = m0 + i;
-  const int64_t row0 = int64_t(blockIdx.x) * 16;
+  int64_t row0 = int64_t(blockIdx.x) * 16;
 
   // DMA lane roles: slice q of a chunk holds rows 2q, 2q+1 (lanes 0-31, 32-63);
   // lane piece cs = lane & 31 stores the row's 16-byte piece cs ^ r.
   const int dr = lane >> 5, cs = lane & 31;
   const uint16_t* wrow[T][kMfmaSlices];
+  auto set_rows = [&](int64_t r0) {
 #pragma unroll
-  for (int t = 0; t < T; ++t)
+    for (int t = 0; t < T; ++t)
 #pragma unroll
-    for (int q = 0; q < kMfmaSlices; ++q) {
-      int64_t row = row0 + 2 * q + dr;
-      if (row >= a.N) row = a.N - 1;
-      wrow[t][q] = ((SILU && t == 1) ? a.W2 : a.W) + row * a.K;
-    }
+      for (int q = 0; q < kMfmaSlices; ++q) {
+        int64_t row = r0 + 2 * q + dr;
+        if (row >= a.N) row = a.N - 1;
+        wrow[t][q] = ((SILU && t == 1) ? a.W2 : a.W) + row * a.K;
+      }
+  };
+  set_rows(row0);
   // Rows past M read row 0: their outputs are never stored.
   const uint16_t* xrow = a.X + (m < a.M ? m : 0) * a.ldx;
 
@@ -330,6 +336,62 @@ __global__ __launch_bounds__(NW * kWave) void linear_mfma_kernel(LinearArgs a) {
   // next chunk's loads outstanding.  CPW > 0 (chunks per wave known at
   // compile time: the model shapes) unrolls the ring completely.
   u32x4v_t xa[kMfmaSteps], xb[kMfmaSteps];
+  auto epilogue = [&](int64_t r0) {
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) red[wave][t][j][lane] = acc[t][j];
+    __syncthreads();
+    // Thread tid < 256 finalises output (j, l) = (tid / 64, tid % 64).
+    if (threadIdx.x < 4 * kWave) {
+      const int j = threadIdx.x >> 6, l = threadIdx.x & 63;
+      const int64_t mo = m0 + (l & 15);
+      const int64_t n = r0 + 4 * (l >> 4) + j;
+      if (mo < a.M && n < a.N) {
+        float v[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          float sacc = 0.f;
+#pragma unroll
+          for (int w = 0; w < NW; ++w) sacc += red[w][t][j][l];
+          v[t] = sacc;
+        }
+        store_out(a, mo, n, v[0], SILU ? v[1] : 0.f);
+      }
+    }
+  };
+  if constexpr (TPB > 1) {
+    static_assert(CPW > 0, "multi-tile blocks need the unrolled ring");
+    constexpr int NC = TPB * CPW;
+    const int64_t stride = int64_t(gridDim.x) * 16;
+    int64_t rn = row0;  // rows of the chunk the next DMA belongs to
+    auto dma_idx = [&](int idx, uint4 (*stage)[kMfmaSlices][kWave]) {
+      const int64_t r = row0 + int64_t(idx / CPW) * stride;
+      if (r != rn) {
+        rn = r;
+        set_rows(r);
+      }
+      dma(cb + idx % CPW, stage);
+      xload(cb + idx % CPW, (idx & 1) ? xb : xa);
+    };
+    dma_idx(0, Wl0[wave]);
+    dma_idx(1, Wl1[wave]);
+#pragma unroll
+    for (int idx = 0; idx < NC; ++idx) {
+      if (idx + 1 < NC) wait_vm<DN + XN>(); else wait_vm<0>();
+      auto& x = (idx & 1) ? xb : xa;
+      auto* stage = (idx & 1) ? Wl1[wave] : Wl0[wave];
+      compute(cb + idx % CPW, stage, x);
+      if (idx + 2 < NC) dma_idx(idx + 2, stage);
+      if (idx % CPW == CPW - 1) {  // tile done: reduce across waves and store
+        epilogue(row0 + int64_t(idx / CPW) * stride);
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        __syncthreads();  // red is rewritten by the next tile
+      }
+    }
+    return;
+  }
   if constexpr (CPW > 0) {
     dma(cb, Wl0[wave]);
     xload(cb, xa);
@@ -375,27 +437,7 @@ __global__ __launch_bounds__(NW * kWave) void linear_mfma_kernel(LinearArgs a) {
     }
   }
 
-#pragma unroll
-  for (int t = 0; t < T; ++t)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) red[wave][t][j][lane] = acc[t][j];
-  __syncthreads();
-
-  // Thread tid < 256 finalises output (j, l) = (tid / 64, tid % 64).
-  if (threadIdx.x >= 4 * kWave) return;
-  const int j = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const int64_t mo = m0 + (l & 15);
-  if (mo >= a.M) return;
-  float v[T];
-#pragma unroll
-  for (int t = 0; t < T; ++t) {
-    float sacc = 0.f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) sacc += red[w][t][j][l];
-    v[t] = sacc;
-  }
-  const int64_t n = row0 + 4 * (l >> 4) + j;
-  if (n < a.N) store_out(a, mo, n, v[0], SILU ? v[1] : 0.f);
+  epilogue(row0);
 }
 
 // ---------------------------------------------------------------------------
@@ -602,13 +644,13 @@ void launch_valu_m(const LinearArgs& a, hipStream_t s) {
   }
 }
 
-template <bool SILU, int NW>
+template <bool SILU, int NW, int TPB = 1>
 void launch_mfma_nw(const LinearArgs& a, hipStream_t s) {
   constexpr int T = SILU ? 2 : 1;
   const dim3 grid(unsigned((a.N + 15) / 16), unsigned((a.M + 15) / 16)), block(NW * kWave);
   const int64_t nchunks = (a.K + kMfmaKC - 1) / kMfmaKC;
   const int64_t cpw = nchunks % NW == 0 ? nchunks / NW : 0;
-#define EZ_MFMA_LAUNCH(C) hipLaunchKernelGGL((linear_mfma_kernel<T, SILU, C, NW>), grid, block, 0, s, a)
+#define EZ_MFMA_LAUNCH(C) hipLaunchKernelGGL((linear_mfma_kernel<T, SILU, C, NW, 1>), grid, block, 0, s, a)
   switch (cpw) {
     case 1: EZ_MFMA_LAUNCH(1); break;
     case 2: EZ_MFMA_LAUNCH(2); break;
@@ -626,6 +668,16 @@ void launch_mfma_nw(const LinearArgs& a, hipStream_t s) {
 template <bool SILU>
 void launch_mfma(const LinearArgs& a, hipStream_t s) {
   if constexpr (SILU) {
+    // gate/up of the model shapes (K = 4096: 4 chunks per wave): 3 or 2
+    // tiles per CU run as multi-tile blocks, one per CU.
+    const int64_t tx = (a.N + 15) / 16, cus = num_cus();
+    const int64_t nchunks = (a.K + kMfmaKC - 1) / kMfmaKC;
+    if (nchunks == 16 && a.K % kMfmaKC == 0 && (tx == 3 * cus || tx == 2 * cus)) {
+      const dim3 grid(unsigned(cus), unsigned((a.M + 15) / 16)), block(4 * kWave);
+      if (tx == 3 * cus) hipLaunchKernelGGL((linear_mfma_kernel<2, true, 4, 4, 3>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((linear_mfma_kernel<2, true, 4, 4, 2>), grid, block, 0, s, a);
+      return;
+    }
     launch_mfma_nw<true, 4>(a, s);
   } else {
     const int64_t tiles = ((a.N + 15) / 16) * ((a.M + 15) / 16), cus = num_cus();

@@ -286,3 +286,30 @@ def test_linear_stage_epilogues(M, epi, norm, N, K):
     _hip.call("ezops_linear_stage_bf16", tX.data_ptr(), K, tW.data_ptr(), tW2.data_ptr(), Y.data_ptr(), N,
               tR.data_ptr(), N, tw.data_ptr(), norm, 1e-6, epi, M, N, K, ws.data_ptr(), ws.numel(), _hip.stream())
     np.testing.assert_allclose(n(Y), ref, rtol=2e-2, atol=3e-2)
+
+
+@pytest.mark.parametrize("M,N", [(16, 12288), (20, 8192), (8, 12288)])
+def test_linear_stage_swiglu_multi_tile(M, N):
+    """Gate/up shapes whose 16-row tiles are 3x / 2x the CU count run as
+    multi-tile blocks (the DMA ring continues across tiles): bit-exact with
+    the one-tile-per-block launch on the same rows, and against the oracle."""
+    K = 4096
+    rng = np.random.default_rng(M + N)
+    X = oracle.bf16(rng.standard_normal((M, K)).astype(np.float32))
+    W = oracle.bf16(rng.standard_normal((N, K)).astype(np.float32) * K ** -0.5)
+    W2 = oracle.bf16(rng.standard_normal((N, K)).astype(np.float32) * K ** -0.5)
+    g_, u = oracle.linear_bf16(X, W), oracle.linear_bf16(X, W2)
+    ref = oracle.bf16(oracle.bf16(g_ / (1 + np.exp(-g_.astype(np.float64)))) * u)
+    tX, tW, tW2 = g(X), g(W), g(W2)
+    ws = torch.zeros(256, dtype=torch.uint8, device=DEV)
+
+    def run(rows):  # the first `rows` output rows through ezops_linear_stage_bf16 (SwiGLU epilogue)
+        Y = torch.empty(M, rows, dtype=torch.bfloat16, device=DEV)
+        _hip.call("ezops_linear_stage_bf16", tX.data_ptr(), K, tW.data_ptr(), tW2.data_ptr(), Y.data_ptr(), rows,
+                  None, 0, None, 0, 1e-6, 2, M, rows, K, ws.data_ptr(), ws.numel(), _hip.stream())
+        return Y
+
+    Y = run(N)
+    np.testing.assert_allclose(n(Y), ref, rtol=2e-2, atol=3e-2)
+    # N - 16 rows: not a multiple of the CU count, so one tile per block
+    assert torch.equal(Y[:, : N - 16], run(N - 16))
