@@ -216,14 +216,45 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
   __shared__ __align__(16) uint16_t Qs[LAYER ? G : 1][D];
   __shared__ __align__(16) uint16_t Kn[LAYER ? D : 1], Vn[LAYER ? D : 1];
 
-  const int split = int(blockIdx.x % unsigned(nsplit)), unit = int(blockIdx.x / unsigned(nsplit));
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   EZ_TRACE(0);
   const int li = lane & 15, lg = lane >> 4;
   const int dc = lane % CPR, rs = lane / CPR;
-  const int kvh = unit % int(a.Hkv);
-  int b = unit / int(a.Hkv);
-  if (a.sort_lens) b = rank_to_seq(a.kv_lens, int(a.B), b, lane);
+  int split, kvh, b, nsb = nsplit;  // nsb: splits of this block's sequence
+  if (a.split_chunk > 0) {
+    // Ragged batch (B <= 64), splits in proportion to the lengths: sequence
+    // j gets ns_j = ceil(len_j / split_chunk) splits per kv head; blocks run
+    // longest sequence first, (kv head, split) within; blocks past the
+    // active ones leave before loading anything.  Lane j < B holds
+    // sequence j's length, rank and first block.
+    const int B = int(a.B);
+    int32_t Lj = lane < B ? a.kv_lens[lane] : 0;
+    Lj = Lj < 0 ? 0 : (int64_t(Lj) > a.Lh ? int32_t(a.Lh) : Lj);
+    int rank = 0;
+    for (int m = 0; m < B; ++m) {
+      const int32_t Lo = __builtin_amdgcn_readlane(Lj, m);
+      rank += (Lo > Lj) || (Lo == Lj && m < lane);
+    }
+    int ns = int((int64_t(Lj) + a.split_chunk - 1) / a.split_chunk);
+    ns = ns < 1 ? 1 : (ns > nsplit ? nsplit : ns);
+    int start = 0;
+    for (int m = 0; m < B; ++m)
+      start += __builtin_amdgcn_readlane(rank, m) < rank ? __builtin_amdgcn_readlane(ns, m) * int(a.Hkv) : 0;
+    const int blk = int(blockIdx.x);
+    const uint64_t hit = __ballot(lane < B && blk >= start && blk < start + ns * int(a.Hkv));
+    if (!hit) return;  // beyond the active blocks (uniform over the block)
+    b = __ffsll(static_cast<unsigned long long>(hit)) - 1;
+    nsb = __builtin_amdgcn_readlane(ns, b);
+    const int off = blk - __builtin_amdgcn_readlane(start, b);
+    kvh = off / nsb;
+    split = off % nsb;
+  } else {
+    split = int(blockIdx.x % unsigned(nsplit));
+    const int unit = int(blockIdx.x / unsigned(nsplit));
+    kvh = unit % int(a.Hkv);
+    b = unit / int(a.Hkv);
+    if (a.sort_lens) b = rank_to_seq(a.kv_lens, int(a.B), b, lane);
+  }
   // The length is requested first, ahead of this wave's tile loads, and
   // unconditionally (a dummy address without kv_lens), so that nothing waits
   // for it before its first use.
@@ -242,7 +273,7 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
   }
   const int64_t h0 = int64_t(kvh) * G;  // first query head of the group
   const float sl2 = a.scale * kLog2e;
-  const int64_t stride = int64_t(nsplit) * W * kTile;  // distance between a wave's tiles
+  const int64_t stride = int64_t(nsb) * W * kTile;  // distance between a wave's tiles
 
   int64_t t0 = (int64_t(split) * W + wave) * kTile;
   uint4 kf[NSUB][NS], vf[NPV];
@@ -471,7 +502,14 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
       a.Out[out_index(a, hq, d)] = f2bf(lv > 0.f ? ov / lv : 0.f);
     } else {
       opart[(hq * nsplit + split) * D + d] = ov;
-      if (d == 0) *reinterpret_cast<float2*>(ml + (hq * nsplit + split) * 2) = make_float2(M, lv);
+      if (d == 0) {
+        *reinterpret_cast<float2*>(ml + (hq * nsplit + split) * 2) = make_float2(M, lv);
+        // the last split of a sequence with fewer than nsplit marks the
+        // unused merge slots empty (weight 0, their partials never read)
+        if (split == nsb - 1)
+          for (int s2 = nsb; s2 < nsplit; ++s2)
+            *reinterpret_cast<float2*>(ml + (hq * nsplit + s2) * 2) = make_float2(-INFINITY, 0.f);
+      }
     }
   }
   EZ_TRACE(6);
@@ -505,7 +543,7 @@ __global__ __launch_bounds__(D) void attn_combine_kernel(AttnArgs a, int nsplit,
 #pragma unroll
   for (int s = 0; s < kMaxSplits; ++s) {
     const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), s));
-    acc = fmaf(w, v[s], acc);  // v[s] = 0 and w = 0 for s >= nsplit
+    acc = w != 0.f ? fmaf(w, v[s], acc) : acc;  // empty splits: weight 0, partial never used
   }
   a.Out[out_index(a, hq, d)] = f2bf(acc);
 }
@@ -582,6 +620,8 @@ int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
   aa.sort_lens = a.kv_lens && a.B > 1 && a.B <= kWave;
   if (aa.scale <= 0.f) aa.scale = 1.0f / sqrtf(float(a.D));
   const SplitPlan pl = plan_splits(aa.B, aa.Hkv, aa.Lh, G);
+  // ragged batches: splits in proportion to each sequence's length
+  aa.split_chunk = (aa.sort_lens && pl.nsplit > 1) ? (aa.Lh + pl.nsplit - 1) / pl.nsplit : 0;
   float *opart = nullptr, *ml = nullptr;
   if (pl.nsplit > 1) {
     const size_t need = attn_workspace_size(a.B, a.H, a.Hkv, a.S, a.D);

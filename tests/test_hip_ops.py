@@ -169,6 +169,24 @@ def test_attn_decode_consecutive_calls_fresh_partials(B, S):
         np.testing.assert_allclose(n(out)[:, :, 0], ref, **BF_TOL)
 
 
+def test_attn_decode_ragged_splits_follow_lengths():
+    """Ragged batches get splits in proportion to each sequence's length;
+    consecutive calls whose lengths shrink leave stale partials of the
+    previous call in the unused split slots, which must never be merged."""
+    B, S = 12, 8192
+    op = AttnDecodeOp(B, 32, S, 128, backend="hip", num_kv_heads=8)
+    torch.manual_seed(21)
+    Q, K, V = op.gen_data()
+    nK, nV = n(K), n(V)
+    rng = np.random.default_rng(21)
+    for it, hi in enumerate([S, S // 2, 600, S]):
+        lens = torch.from_numpy(rng.integers(1, hi + 1, size=B).astype(np.int32))
+        lens[it % B] = hi
+        out = op._kernel(Q, K, V, lens.to(DEV), max_kv_len=S)
+        ref = oracle.attn_decode(n(Q)[:, :, 0], nK, nV, lens.numpy().astype(np.int64))
+        np.testing.assert_allclose(n(out)[:, :, 0], ref, **BF_TOL)
+
+
 def test_reduce_consecutive_calls():
     op = ReduceOp(1 << 22, backend="hip")
     Out = torch.empty(1, device=DEV)
