@@ -34,6 +34,9 @@
 #include "status.h"
 #include "../../include/ezops_hip.h"
 
+#ifndef EZ_ATTN_TARGET4
+#define EZ_ATTN_TARGET4 8  // 4-wave blocks planned per CU
+#endif
 #ifndef EZ_ATTN_TRACE
 #define EZ_ATTN_TRACE 0  // timing experiments only: per-wave phase timestamps
 #endif
@@ -562,7 +565,7 @@ SplitPlan plan_splits(int64_t B, int64_t Hkv, int64_t Lh, int64_t G) {
   // 8-wave blocks for few units; group 8 keeps 4 waves (its accumulators need
   // the register budget of one wave per SIMD).
   const int waves = (units * 4 <= cus && G <= 4) ? 8 : 4;
-  const int64_t target = waves == 8 ? 2 * cus : 8 * cus;  // blocks in flight
+  const int64_t target = waves == 8 ? 2 * cus : EZ_ATTN_TARGET4 * cus;  // blocks in flight
   int64_t ns = (target + units - 1) / units;
   const int64_t max_ns = (Lh + int64_t(waves) * kTile - 1) / (int64_t(waves) * kTile);
   if (ns > max_ns) ns = max_ns;
