@@ -52,3 +52,34 @@ def test_workspace_sizes():
     assert lib.ezops_attn_decode_workspace_size(0, 32, 8, 8192, 128) == 0
     p = _hip.Qwen3LayerParams(B=1, S=16384, HS=4096, IS=12288, H=32, Hkv=8, D=128)
     assert lib.ezops_qwen3_layer_workspace_size(ctypes.byref(p)) > 12288 * 2
+
+
+def test_new_entry_points_reject_bad_arguments():
+    """Validation of the paged / prefill / step / GEMM entries happens before
+    any device call, so it runs without a GPU.  Non-null dummy pointers are
+    never dereferenced on these paths."""
+    lib = _hip.lib()
+    d = 64  # a non-null address that is never touched
+    # paged attention: page size must be a power of two >= 32
+    rc = lib.ezops_paged_attn_decode_bf16(d, d, d, d, d, d, 2, 32, 8, 128, 16, 48, 4, 0, 0.0, d, 1 << 20, None)
+    assert rc == _hip.EINVAL and b"page_size" in lib.ezops_hip_last_error()
+    # prefill attention: head_dim 128 only
+    rc = lib.ezops_prefill_attn_bf16(d, d, d, d, d, None, 1, 16, 8, 8, 64, 64, 16, None, 0, 0, 0.0, None)
+    assert rc == _hip.EINVAL and b"head_dim" in lib.ezops_hip_last_error()
+    # library GEMM: empty shapes
+    assert lib.ezops_gemm_bf16(d, 16, d, d, 16, None, 0, 16, 16, d, 1 << 20, None) == _hip.EINVAL
+    # layer prefill: cu_seqlens is required
+    p = _hip.Qwen3LayerParams(B=1, S=128, HS=256, IS=512, H=4, Hkv=2, D=128, hidden=d, K_cache=d, V_cache=d,
+                              Wqkv=d, Wo=d, Wgu=d, Wd=d, out=d)
+    assert lib.ezops_qwen3_prefill_bf16(ctypes.byref(p), 16, None, 16, None, 0, 0, d, 1 << 20, None) == _hip.EINVAL
+    # decode step: layers must share one shape, and there must be at least one
+    layers = (_hip.Qwen3LayerParams * 2)()
+    for i, hs in enumerate((256, 512)):
+        layers[i] = _hip.Qwen3LayerParams(B=1, S=128, HS=hs, IS=512, H=4, Hkv=2, D=128, hidden=d, out=d)
+    rc = lib.ezops_qwen3_decode_step_bf16(layers, 2, None, 0, 0, None, None, 0, None, d, 1 << 20, None)
+    assert rc == _hip.EINVAL and b"shape" in lib.ezops_hip_last_error()
+    assert lib.ezops_qwen3_decode_step_bf16(layers, 0, None, 0, 0, None, None, 0, None, d, 1 << 20, None) == _hip.EINVAL
+    # a paged decode step needs page_size a power of two dividing S
+    same = (_hip.Qwen3LayerParams * 1)()
+    same[0] = _hip.Qwen3LayerParams(B=1, S=128, HS=256, IS=512, H=4, Hkv=2, D=128, hidden=d, out=d)
+    assert lib.ezops_qwen3_decode_step_bf16(same, 1, d, 4, 48, None, None, 0, None, d, 1 << 30, None) == _hip.EINVAL
