@@ -118,3 +118,14 @@ def test_paged_layer_equals_contiguous(batch, seq_len, page_size):
         touched[int(bt[b, (L - 1) // page_size]), (L - 1) % page_size] = True
     rows = lambda t: t.transpose(1, 2)[~touched]  # noqa: E731  (page, row) pairs not written
     assert torch.equal(rows(data[1]), rows(K0)) and torch.equal(rows(data[2]), rows(V0))
+
+
+def test_paged_attn_deterministic_and_inputs_read_only():
+    op = PagedAttnDecodeOp(4, 32, 8, 128, page_size=64, max_pages=32, num_pages=160, backend="hip")
+    torch.manual_seed(31)
+    data = op.gen_data()
+    before = [t.clone() for t in data]
+    a = op(*data, max_kv_len=2048)
+    b = op(*data, max_kv_len=2048)
+    assert torch.equal(a, b)
+    assert all(torch.equal(x, y) for x, y in zip(data, before))

@@ -146,3 +146,32 @@ def test_prefill_attn_clamps_device_lengths():
     _hip.call("ezops_prefill_attn_bf16", Q.data_ptr(), K.data_ptr(), V.data_ptr(), out2.data_ptr(),
               cu_over.data_ptr(), None, 2, 150, 32, 8, 512, 128, 100, None, 0, 0, 0.0, _hip.stream())
     assert torch.equal(out2, ref)
+
+
+def test_prefill_deterministic_and_writes_only_chunk_rows():
+    """Prefill attention leaves its inputs untouched and repeats bit-for-bit;
+    the prefill layer writes exactly the chunk's cache rows and repeats
+    bit-for-bit from the same starting cache."""
+    torch.manual_seed(33)
+    at = PrefillAttnOp(2, 32, 8, 128, 1024, [200, 77], [100, 0], backend="hip")
+    data = at.gen_data()
+    before = [t.clone() for t in data]
+    x, y = at(*data), at(*data)
+    assert torch.equal(x, y) and all(torch.equal(u, v) for u, v in zip(data, before))
+
+    q_lens, past = [130, 20], [0, 500]
+    op = Qwen3PrefillOp(2, 1024, q_lens=q_lens, past_lens=past, backend="hip", num_kv_heads=8, norm_weights=True,
+                        rope_theta=1e6, **QWEN3_8B)
+    d = list(op.gen_data())
+    K0, V0 = d[1].clone(), d[2].clone()
+    out1 = op(*d)
+    K1, V1 = d[1].clone(), d[2].clone()
+    d[1].copy_(K0)
+    d[2].copy_(V0)
+    out2 = op(*d)
+    assert torch.equal(out1, out2) and torch.equal(d[1], K1) and torch.equal(d[2], V1)
+    touched = torch.zeros(2, 1024, dtype=torch.bool, device="cuda")
+    for b_, (n_, p_) in enumerate(zip(q_lens, past)):
+        touched[b_, p_:p_ + n_] = True
+    rows = lambda t: t.transpose(1, 2)[~touched]  # noqa: E731
+    assert torch.equal(rows(K1), rows(K0)) and torch.equal(rows(V1), rows(V0))
