@@ -9,8 +9,11 @@
 // B = X^T viewed as K x M (ld ldx).
 //
 // One handle per device and one algorithm per shape are set up on first use
-// (host-side heuristic query) and cached; a caller that captures a graph
-// runs the shape once eagerly first.
+// and cached: the first eager call of a shape times up to kTune candidates
+// from hipBLASLt's heuristic on the caller's stream (a one-time host wait)
+// and keeps the fastest; a first call under graph capture, or with the
+// residual aliasing the output, takes the heuristic's first choice.  A
+// caller that captures a graph runs the shape once eagerly first.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
@@ -32,6 +35,7 @@ struct Plan {
   size_t ws = 0;
 };
 
+constexpr int kTune = 8;
 using Key = std::tuple<int, int64_t, int64_t, int64_t, int64_t, int64_t, bool, size_t>;
 std::mutex g_mu;
 std::map<int, hipblasLtHandle_t> g_handles;
@@ -43,8 +47,29 @@ std::map<Key, Plan> g_plans;
     EZ_REQUIRE(st_ == HIPBLAS_STATUS_SUCCESS, "gemm: %s failed (status %d)", #call, int(st_)); \
   } while (0)
 
+// Time one candidate: a warm-up and 3 runs between events on the stream.
+float time_algo(hipblasLtHandle_t h, const Plan& p, const hipblasLtMatmulAlgo_t& algo, size_t ws_need,
+                const uint16_t* X, const uint16_t* W, uint16_t* Y, const uint16_t* R, void* ws, hipStream_t s) {
+  const float alpha = 1.f, beta = R ? 1.f : 0.f;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -1.f;
+  float ms = -1.f;
+  bool ok = hipblasLtMatmul(h, p.desc, &alpha, W, p.a, X, p.b, &beta, R ? R : Y, p.c, Y, p.c, &algo,
+                            ws_need ? ws : nullptr, ws_need, s) == HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipEventRecord(e0, s) == hipSuccess;
+  for (int i = 0; ok && i < 3; ++i)
+    ok = hipblasLtMatmul(h, p.desc, &alpha, W, p.a, X, p.b, &beta, R ? R : Y, p.c, Y, p.c, &algo,
+                         ws_need ? ws : nullptr, ws_need, s) == HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
+  ok = ok && hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  return ok ? ms : -1.f;
+}
+
 int get_plan(int dev, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy, bool resid, size_t ws_cap,
-             hipblasLtHandle_t* h, const Plan** out) {
+             hipblasLtHandle_t* h, const Plan** out, const uint16_t* X, const uint16_t* W, uint16_t* Y,
+             const uint16_t* R, void* ws, hipStream_t s) {
   std::lock_guard<std::mutex> lk(g_mu);
   auto hit = g_handles.find(dev);
   if (hit == g_handles.end()) {
@@ -71,14 +96,29 @@ int get_plan(int dev, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy,
   EZ_LT(hipblasLtMatmulPreferenceCreate(&pref));
   const uint64_t cap = ws_cap;
   EZ_LT(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &cap, sizeof(cap)));
-  hipblasLtMatmulHeuristicResult_t res[1];
+  hipblasLtMatmulHeuristicResult_t res[kTune];
   int n = 0;
-  const hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(*h, p.desc, p.a, p.b, p.c, p.c, pref, 1, res, &n);
+  const hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(*h, p.desc, p.a, p.b, p.c, p.c, pref, kTune, res, &n);
   hipblasLtMatmulPreferenceDestroy(pref);
   EZ_REQUIRE(st == HIPBLAS_STATUS_SUCCESS && n >= 1, "gemm: no hipBLASLt algorithm for M=%lld N=%lld K=%lld",
              (long long)M, (long long)N, (long long)K);
-  p.algo = res[0].algo;
-  p.ws = res[0].workspaceSize;
+  int best = 0;
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  const bool tune =
+      n > 1 && R != Y && hipStreamIsCapturing(s, &capture) == hipSuccess && capture == hipStreamCaptureStatusNone;
+  if (tune) {
+    float best_ms = -1.f;
+    for (int i = 0; i < n; ++i) {
+      if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > ws_cap) continue;
+      const float ms = time_algo(*h, p, res[i].algo, res[i].workspaceSize, X, W, Y, R, ws, s);
+      if (ms > 0.f && (best_ms < 0.f || ms < best_ms)) {
+        best_ms = ms;
+        best = i;
+      }
+    }
+  }
+  p.algo = res[best].algo;
+  p.ws = res[best].workspaceSize;
   *out = &g_plans.emplace(key, p).first->second;
   return 0;
 }
@@ -93,7 +133,7 @@ int gemm_bf16(const uint16_t* X, int64_t ldx, const uint16_t* W, uint16_t* Y, in
   EZ_REQUIRE(hipGetDevice(&dev) == hipSuccess, "gemm: no current device");
   hipblasLtHandle_t h = nullptr;
   const Plan* p = nullptr;
-  const int rc = get_plan(dev, M, N, K, ldx, ldy, R != nullptr, ws ? ws_bytes : 0, &h, &p);
+  const int rc = get_plan(dev, M, N, K, ldx, ldy, R != nullptr, ws ? ws_bytes : 0, &h, &p, X, W, Y, R, ws, s);
   if (rc) return rc;
   const float alpha = 1.f, beta = R ? 1.f : 0.f;
   EZ_LT(hipblasLtMatmul(h, p->desc, &alpha, W, p->a, X, p->b, &beta, R ? R : Y, p->c, Y, p->c, &p->algo,
