@@ -11,6 +11,8 @@
 //                 S^T registers: the k slots 8h..8h+7 of a 16-key step are
 //                 keys 4h..4h+3 and 8+4h..8+4h+3 of it, the same slot order
 //                 in A and B, so P never leaves the lane.
+// Probabilities use the hardware v_exp_f32 directly (results below 2^-126 of
+// the row maximum flush to zero, far below what the bf16 P operand holds).
 // Queries sit in the lane column j in both products, so a query's running
 // max / sum and its output column share the lane: the only cross-lane step
 // is the swap between the lane halves j and j+32.
@@ -118,14 +120,24 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
   // 4*vm .. 4*vm+3 (vm = tid/16), dims 8*vc .. 8*vc+7 (vc = tid%16)
   uint4 kr[4], vr[4];
   const int vm = tid >> 4, vc = tid & 15;
+  // contiguous cache: the (sequence, kv head) slabs, rows addressed in 32 bits
+  const uint16_t* kslab = a.K + (int64_t(b) * a.Hkv + kvh) * a.S * kPD;
+  const uint16_t* vslab = a.V + (int64_t(b) * a.Hkv + kvh) * a.S * kPD;
+  const int kend32 = int(kend);
   auto load_tile = [&](int64_t k0) {
+    const int k032 = int(k0);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int id = tid + c * kPW * kWave;
-      const int64_t row = min(k0 + (id >> 4), kend - 1);
-      kr[c] = *reinterpret_cast<const uint4*>(cache_row<PAGED>(a, a.K, b, kvh, row) + (id & 15) * 8);
-      const int64_t vrow = min(k0 + 4 * vm + c, kend - 1);
-      vr[c] = *reinterpret_cast<const uint4*>(cache_row<PAGED>(a, a.V, b, kvh, vrow) + vc * 8);
+      const int row = min(k032 + (id >> 4), kend32 - 1);
+      const int vrow = min(k032 + 4 * vm + c, kend32 - 1);
+      if constexpr (PAGED) {
+        kr[c] = *reinterpret_cast<const uint4*>(cache_row<PAGED>(a, a.K, b, kvh, row) + (id & 15) * 8);
+        vr[c] = *reinterpret_cast<const uint4*>(cache_row<PAGED>(a, a.V, b, kvh, vrow) + vc * 8);
+      } else {
+        kr[c] = *reinterpret_cast<const uint4*>(kslab + uint32_t(row * kPD + (id & 15) * 8));
+        vr[c] = *reinterpret_cast<const uint4*>(vslab + uint32_t(vrow * kPD + vc * 8));
+      }
     }
   };
   auto store_tile = [&](int buf) {
@@ -186,7 +198,7 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[kk][r]);
       mx = halves_max(mx);
       const float mn = fmaxf(m, mx * sl2);  // finite: key 0 is visible to every query
-      const float alpha = exp2f(m - mn);
+      const float alpha = __builtin_amdgcn_exp2f(m - mn);
       m = mn;
       l *= alpha;
       if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // rescale only when some row max moved
@@ -201,8 +213,8 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
           uint32_t w[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const float p0 = exp2f(fmaf(st[kk][8 * u + 2 * q], sl2, -mn));
-            const float p1 = exp2f(fmaf(st[kk][8 * u + 2 * q + 1], sl2, -mn));
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(st[kk][8 * u + 2 * q], sl2, -mn));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(st[kk][8 * u + 2 * q + 1], sl2, -mn));
             l += p0 + p1;
             w[q] = cvt_bf2(p0, p1);
           }
