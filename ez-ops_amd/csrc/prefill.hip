@@ -64,6 +64,44 @@ __device__ __forceinline__ const uint16_t* cache_row(const PrefillAttnArgs& a, c
   return base + ((int64_t(id) * a.Hkv + kvh) * a.page_size + (row - (pg << sh))) * kPD;
 }
 
+typedef unsigned int u32x4v_t __attribute__((ext_vector_type(4)));
+
+// Reads 8 K fragments from LDS and waits for them.  One asm block without a
+// memory clobber: the compiler's own wait insertion treats any LDS read after
+// an LDS DMA as dependent on every outstanding load and would wait (vmcnt 0)
+// for the next tile's prefetch here; these reads touch the other buffer, and
+// the volatile asm keeps its place between the barriers that order them
+// against the DMA into that buffer.
+__device__ __forceinline__ void lds_read8(const uint32_t (&addr)[8], u32x4v_t (&r)[8]) {
+  asm volatile(
+      "ds_read_b128 %0, %8\n\t"
+      "ds_read_b128 %1, %9\n\t"
+      "ds_read_b128 %2, %10\n\t"
+      "ds_read_b128 %3, %11\n\t"
+      "ds_read_b128 %4, %12\n\t"
+      "ds_read_b128 %5, %13\n\t"
+      "ds_read_b128 %6, %14\n\t"
+      "ds_read_b128 %7, %15\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+      : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]), "v"(addr[5]), "v"(addr[6]),
+        "v"(addr[7]));
+}
+static_assert(kPD / 16 == 8, "lds_read8 reads the 8 k-steps of a 128-dim key row");
+// Reads 4 V^T fragments (two 8-byte halves 16 bytes apart each) from LDS
+// and waits for them; an asm block for the same reason as lds_read8.
+__device__ __forceinline__ void lds_read_vt4(const uint32_t (&addr)[4], u32x4v_t (&r)[4]) {
+  asm volatile(
+      "ds_read2_b64 %0, %4 offset1:2\n\t"
+      "ds_read2_b64 %1, %5 offset1:2\n\t"
+      "ds_read2_b64 %2, %6 offset1:2\n\t"
+      "ds_read2_b64 %3, %7 offset1:2\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+      : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]));
+}
+static_assert(kPD / 32 == 4, "lds_read_vt4 reads the 4 dimension blocks of a 128-dim head");
+
 // Block = (query tile, sequence, kv head, head group of HPB = min(G, 4) query
 // heads); wave w serves query head kvh*G + hb*HPB + w%HPB, query rows
 // 32*(w/HPB) .. +31 of the tile (BQ = 32 * 4/HPB rows).  K/V tiles of 64
@@ -118,69 +156,82 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
 
   // staging: K chunks id = tid + 256c -> key id/16, chunk id%16; V: keys
   // 4*vm .. 4*vm+3 (vm = tid/16), dims 8*vc .. 8*vc+7 (vc = tid%16)
-  uint4 kr[4], vr[4];
+  uint4 vr[4];
   const int vm = tid >> 4, vc = tid & 15;
   // contiguous cache: the (sequence, kv head) slabs, rows addressed in 32 bits
   const uint16_t* kslab = a.K + (int64_t(b) * a.Hkv + kvh) * a.S * kPD;
   const uint16_t* vslab = a.V + (int64_t(b) * a.Hkv + kvh) * a.S * kPD;
   const int kend32 = int(kend);
-  auto load_tile = [&](int64_t k0) {
+  // K goes straight to LDS (global_load_lds_dwordx4): load c of wave w fills
+  // LDS chunks 256c + 64w .. +63, one per lane, so lane tid writes chunk
+  // p = 256c + tid = (key p/16, swizzled slot p%16) and reads the global
+  // chunk (p%16) ^ (key & 15) of that key.  V is staged in registers and
+  // transposed on the LDS store.
+  auto load_tile = [&](int64_t k0, int nb) {
     const int k032 = int(k0);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int id = tid + c * kPW * kWave;
-      const int row = min(k032 + (id >> 4), kend32 - 1);
+      const int r = id >> 4;
+      const int row = min(k032 + r, kend32 - 1);
+      const int cc = (id & 15) ^ (r & 15);
       const int vrow = min(k032 + 4 * vm + c, kend32 - 1);
+      const uint16_t* kp;
       if constexpr (PAGED) {
-        kr[c] = *reinterpret_cast<const uint4*>(cache_row<PAGED>(a, a.K, b, kvh, row) + (id & 15) * 8);
+        kp = cache_row<PAGED>(a, a.K, b, kvh, row) + cc * 8;
         vr[c] = *reinterpret_cast<const uint4*>(cache_row<PAGED>(a, a.V, b, kvh, vrow) + vc * 8);
       } else {
-        kr[c] = *reinterpret_cast<const uint4*>(kslab + uint32_t(row * kPD + (id & 15) * 8));
+        kp = kslab + uint32_t(row * kPD + cc * 8);
         vr[c] = *reinterpret_cast<const uint4*>(vslab + uint32_t(vrow * kPD + vc * 8));
       }
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(kp),
+                                       (__attribute__((address_space(3))) void*)(&Ks[nb][(c * kPW + wave) * kWave * 8]),
+                                       16, 0, 0);
     }
   };
   auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int id = tid + c * kPW * kWave;
-      const int r = id >> 4, cc = id & 15;
-      *reinterpret_cast<uint4*>(&Ks[buf][r * kPD + ((cc ^ (r & 15)) * 8)]) = kr[c];
-    }
-    const uint32_t* v0 = reinterpret_cast<const uint32_t*>(&vr[0]);
-    const uint32_t* v1 = reinterpret_cast<const uint32_t*>(&vr[1]);
-    const uint32_t* v2 = reinterpret_cast<const uint32_t*>(&vr[2]);
-    const uint32_t* v3 = reinterpret_cast<const uint32_t*>(&vr[3]);
+    // word w of a 16-byte chunk, by field
+    auto word = [](const uint4& v, int w) { return w == 0 ? v.x : w == 1 ? v.y : w == 2 ? v.z : v.w; };
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int sh = (e & 1) * 16;
-      const uint32_t k0v = (v0[e >> 1] >> sh) & 0xffffu, k1v = (v1[e >> 1] >> sh) & 0xffffu;
-      const uint32_t k2v = (v2[e >> 1] >> sh) & 0xffffu, k3v = (v3[e >> 1] >> sh) & 0xffffu;
+      const uint32_t k0v = (word(vr[0], e >> 1) >> sh) & 0xffffu, k1v = (word(vr[1], e >> 1) >> sh) & 0xffffu;
+      const uint32_t k2v = (word(vr[2], e >> 1) >> sh) & 0xffffu, k3v = (word(vr[3], e >> 1) >> sh) & 0xffffu;
       *reinterpret_cast<uint2*>(&Vt[buf][(vc * 8 + e) * kVtStride + 4 * vm]) =
           make_uint2(k0v | (k1v << 16), k2v | (k3v << 16));
     }
+    // the K DMA into this buffer has landed before the barrier that follows
+    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
   };
-  load_tile(0);
+  load_tile(0, 0);
   store_tile(0);
   __syncthreads();
 
   int buf = 0;
   for (int64_t k0 = 0; k0 < kend; k0 += kBK, buf ^= 1) {
     const bool more = k0 + kBK < kend;
-    if (more) load_tile(k0 + kBK);  // next tile's global loads overlap this tile's math
+    if (more) load_tile(k0 + kBK, buf ^ 1);  // next tile's global loads overlap this tile's math
 
     if (k0 <= wave_last) {  // a wave whose queries all precede the tile skips it
       f32x16_t st[kBK / 32];
+      const uint32_t ks_base =
+          uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint16_t*)(&Ks[buf][0])));
+      const uint32_t vt_base =
+          uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint16_t*)(&Vt[buf][0])));
+      uint32_t kaddr[kPD / 16];
 #pragma unroll
       for (int kk = 0; kk < kBK / 32; ++kk) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) st[kk][r] = 0.f;
         const int row = 32 * kk + j;  // key row read by this lane (A operand row i = j)
 #pragma unroll
-        for (int s = 0; s < kPD / 16; ++s) {
-          const uint4 kv = *reinterpret_cast<const uint4*>(&Ks[buf][row * kPD + (((2 * s + h) ^ (row & 15)) * 8)]);
-          st[kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kv), qf[s], st[kk], 0, 0, 0);
-        }
+        for (int s = 0; s < kPD / 16; ++s)
+          kaddr[s] = ks_base + uint32_t(row * kPD + (((2 * s + h) ^ (row & 15)) * 8)) * 2;
+        u32x4v_t kf[kPD / 16];
+        lds_read8(kaddr, kf);
+#pragma unroll
+        for (int s = 0; s < kPD / 16; ++s)
+          st[kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[s]), qf[s], st[kk], 0, 0, 0);
       }
       // st[kk][r] = S[query j][key k0 + 32kk + 8(r/4) + 4h + r%4] (unscaled)
       if (k0 + kBK - 1 > past + qi0) {  // diagonal tile: causal mask (32-bit offsets)
@@ -220,14 +271,14 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
           }
           const bf16x8_t pb = as_bf16x8(make_uint4(w[0], w[1], w[2], w[3]));
           const int kc = 32 * kk + 16 * u + 4 * h;
+          uint32_t vaddr[kPD / 32];
 #pragma unroll
-          for (int d = 0; d < kPD / 32; ++d) {
-            const uint16_t* vrow = &Vt[buf][(32 * d + j) * kVtStride + kc];
-            const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
-            const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
-            o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y)), pb,
-                                                           o[d], 0, 0, 0);
-          }
+          for (int d = 0; d < kPD / 32; ++d) vaddr[d] = vt_base + uint32_t((32 * d + j) * kVtStride + kc) * 2;
+          u32x4v_t vf[kPD / 32];
+          lds_read_vt4(vaddr, vf);  // keys kc..kc+3 and kc+8..kc+11 of dims 32d + j
+#pragma unroll
+          for (int d = 0; d < kPD / 32; ++d)
+            o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vf[d]), pb, o[d], 0, 0, 0);
         }
       }
     }
