@@ -9,20 +9,24 @@
 // Lh of the live lengths (the capacity S when no bound is given); the
 // lengths themselves are read on the device.
 //
-// Per wave and tile:
-//   * scores S[h, p] = q_h . k_p on MFMA (v_mfma_f32_16x16x32_bf16): A = the
-//     G query rows (zero-padded to 16), B = 16 positions of K per sub-tile;
-//     a lane loads 16-byte pieces of K rows straight into the B operand
-//     (k-slot (lg, e) of step s = head dim 32 s + 8 lg + e, Q uses the same
-//     map), so one load instruction reads 64 contiguous bytes of 16 rows.
-//   * online softmax in the exp2 domain (scale * log2 e folded into S), the
-//     running max wave-uniform, row maxima by DPP.
-//   * O += P . V on VALU: V rows are read with fully coalesced 16-byte loads
-//     (one wave instruction covers 1 KiB of consecutive rows); P goes through
-//     a small LDS slice per wave and is read back as broadcasts.
+// Per wave and tile (both products on v_mfma_f32_16x16x32_bf16):
+//   * scores, transposed: S^T = K Q^T with A = 16 positions of K per
+//     sub-tile, B = the G query rows (zero-padded to 16 columns); a lane
+//     loads 16-byte pieces of K rows straight into the A operand (k-slot
+//     (lg, e) of step s = head dim 32 s + 8 lg + e, Q uses the same map), so
+//     one load instruction reads 64 contiguous bytes of 16 rows.  Lane
+//     (li, lg) then holds 8 scores of query head li.
+//   * online softmax in the exp2 domain (scale * log2 e folded into S), one
+//     head per lane column: row maxima across the 4 lane groups by lane
+//     swaps, the rescale of O skipped when no running max moved.
+//   * O^T += V^T P^T: the 8 probabilities of a lane, rounded to bf16, are the
+//     B operand as they stand (k-slot 8 lg + e = position 16(e/4) + 4 lg +
+//     e%4); V rows are read with fully coalesced 16-byte loads, stored
+//     row-major into a per-wave LDS slab and read back as the V^T operand by
+//     transposing LDS reads (ds_read_b64_tr_b16), D/16 MFMAs per tile.
 //   * every tile load is unconditional (rows past the live length read a
-//     clamp row): the next tile's K is requested right after the MFMAs and
-//     its V right after P.V, and each wait covers only the data it needs.
+//     clamp row): the next tile's K is requested right after the score MFMAs
+//     and its V right after P.V.
 // The first tile is requested before the length arrives (its addresses only
 // need Lh), behind a single scalar load of the length.  The W waves merge
 // (max, sum, O) through LDS; with more than one split the blocks write fp32
@@ -119,18 +123,51 @@ __device__ __forceinline__ void load_k_tile(const uint16_t* tb, int64_t ts, int6
   }
 }
 
-// V rows in row layout: lane (dc, rs) reads rows rs, rs + RPI, ... of the
-// tile (clamped to `last`), 16 B at column 8*dc.
-template <int D, int NPV>
-__device__ __forceinline__ void load_v_tile(const uint16_t* tb, int64_t ts, int64_t t0, int64_t last, int dc,
-                                            int rs, uint4 (&vf)[NPV]) {
-  constexpr int RPI = kWave / (D / 8);
+// V tiles live in LDS, one slab of kTile rows x D bf16 per wave, row-major
+// with 16-byte chunk c of row p at slot c ^ vswz(p): the transposing reads of
+// the P.V operand (16 lanes over 4 rows x 32 bytes) then cover all banks.
+template <int D>
+__device__ __forceinline__ int vswz(int p) {
+  return (2 * p) & (D / 8 - 1);
+}
+
+// V tile rows t0 + p (clamped to `last`) into registers, in the order of the
+// slab's slots: load i of lane l is slot 64i + l = (row p, slot c'), the
+// chunk c' ^ vswz(p) of that row (each row still read by CPR lanes as one
+// contiguous run).  tb is the first row of the tile at ts = tile_start(t0, last).
+template <int D>
+__device__ __forceinline__ void load_v_regs(const uint16_t* tb, int64_t ts, int64_t t0, int64_t last, int lane,
+                                            uint4 (&v)[kTile * D / 8 / kWave]) {
+  constexpr int CPR = D / 8, RPD = kWave / CPR, VI = kTile / RPD;
 #pragma unroll
-  for (int j = 0; j < NPV; ++j) {
-    int64_t p = t0 + rs + RPI * j;
-    p = p < last ? p : last;
-    vf[j] = ld16_stream(tb + (p - ts) * D + dc * 8);
+  for (int i = 0; i < VI; ++i) {
+    const int p = i * RPD + lane / CPR;
+    int64_t r = t0 + p;
+    r = r < last ? r : last;
+    v[i] = ld16_stream(tb + (r - ts) * D + ((lane % CPR) ^ vswz<D>(p)) * 8);
   }
+}
+
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
+// Four V^T operand halves by transposing LDS reads (ds_read_b64_tr_b16: in
+// each 16-lane group, lane m receives element m%4 of the 8-byte rows that
+// lanes m/4, 4 + m/4, 8 + m/4 and 12 + m/4 address): r[2q] from addr[q],
+// r[2q+1] from addr[q] + 16 rows.  One asm block with its own wait; the
+// caller orders the slab stores before it with a compiler barrier.
+template <int ROW16>
+__device__ __forceinline__ void vt_read4(const uint32_t* addr, i32x2_t (&r)[8]) {
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %8\n\t"
+      "ds_read_b64_tr_b16 %1, %8 offset:%12\n\t"
+      "ds_read_b64_tr_b16 %2, %9\n\t"
+      "ds_read_b64_tr_b16 %3, %9 offset:%12\n\t"
+      "ds_read_b64_tr_b16 %4, %10\n\t"
+      "ds_read_b64_tr_b16 %5, %10 offset:%12\n\t"
+      "ds_read_b64_tr_b16 %6, %11\n\t"
+      "ds_read_b64_tr_b16 %7, %11 offset:%12\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+      : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "i"(ROW16));
 }
 
 // Qwen3 per-head RMSNorm (fp32 statistics, weight) + half-split RoPE of one
@@ -205,24 +242,23 @@ __device__ __forceinline__ int rank_to_seq(const int32_t* lens, int B, int r, in
 template <int D, int G, int W, bool LAYER, bool PAGED>
 __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int nsplit, float* opart, float* ml) {
   EZ_PROF_WAVE(kProfAttnSplit);
-  constexpr int NS = D / 32;         // MFMA k-steps per 16-position sub-tile
-  constexpr int CPR = D / 8;         // 16-byte chunks per K/V row
-  constexpr int RPI = kWave / CPR;   // rows covered by one wave-wide V load
-  constexpr int NSUB = kTile / 16;   // MFMA sub-tiles per tile
-  constexpr int NPV = kTile / RPI;   // V rows per lane per tile
-  constexpr int GP = G <= 4 ? 4 : 8; // P row stride in LDS (float4 reads)
+  constexpr int NS = D / 32;          // MFMA k-steps per 16-position sub-tile of S
+  constexpr int NSUB = kTile / 16;    // sub-tiles per tile
+  constexpr int NDB = D / 16;         // 16-dim blocks of O^T
+  constexpr int VI = kTile * D / 8 / kWave;  // 16-byte V loads per lane and tile
   static_assert(G <= 8, "group size");
+  static_assert(kTile == 32 && NDB % 4 == 0, "tile geometry");
 
-  __shared__ __align__(16) float Ps[W][kTile][GP];
+  __shared__ __align__(16) uint16_t Vs[W][kTile * D];  // per-wave V tile (vswz layout)
   __shared__ __align__(16) float Os[W][G][D];
   __shared__ float Ms[W][G], Ls[W][G];
   __shared__ __align__(16) uint16_t Qs[LAYER ? G : 1][D];
   __shared__ __align__(16) uint16_t Kn[LAYER ? D : 1], Vn[LAYER ? D : 1];
 
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar tile loop
   EZ_TRACE(0);
   const int li = lane & 15, lg = lane >> 4;
-  const int dc = lane % CPR, rs = lane / CPR;
   int split, kvh, b, nsb = nsplit;  // nsb: splits of this block's sequence
   if (a.split_chunk > 0) {
     // Ragged batch (B <= 64), splits in proportion to the lengths: sequence
@@ -277,15 +313,16 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
   const int64_t h0 = int64_t(kvh) * G;  // first query head of the group
   const float sl2 = a.scale * kLog2e;
   const int64_t stride = int64_t(nsb) * W * kTile;  // distance between a wave's tiles
+  uint16_t* slab = &Vs[wave][0];
 
   int64_t t0 = (int64_t(split) * W + wave) * kTile;
-  uint4 kf[NSUB][NS], vf[NPV];
+  uint4 kf[NSUB][NS], vn[VI];
   __builtin_amdgcn_sched_barrier(0);
   {
     const int64_t ts = tile_start(t0, a.Lh - 1);
     const int32_t id = kr.page_id(ts, lane);
     load_k_tile<D, NSUB>(kr.at(ts, id), ts, t0, a.Lh - 1, li, lg, kf);
-    load_v_tile<D, NPV>(vr.at(ts, id), ts, t0, a.Lh - 1, dc, rs, vf);
+    load_v_regs<D>(vr.at(ts, id), ts, t0, a.Lh - 1, lane, vn);
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -340,26 +377,36 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
     }
   }
 
-  float m_run[G], l_acc[G], o[G][8];
+  // Transposing-read addresses (bytes): lane (li, lg) of 16-dim block db
+  // reads row 4lg + li/4, dims 16db + 4(li%4) .. +3; the second half of the
+  // operand is 16 rows further.
+  uint32_t vaddr[NDB];
+  {
+    const uint32_t sbase = uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint16_t*)slab));
+    const int row = 4 * lg + (li >> 2), j = li & 3;
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    m_run[h] = -INFINITY;
-    l_acc[h] = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
+    for (int db = 0; db < NDB; ++db)
+      vaddr[db] = sbase + uint32_t(row * D * 2 + (((2 * db + (j >> 1)) ^ vswz<D>(row)) * 16) + (j & 1) * 8);
   }
+
+  // Lane (li, lg) keeps the state of query head li (heads >= G are padding):
+  // running max, its share of the sum, O^T[16db + 4lg + r][li] in o[db][r].
+  float m_run = -INFINITY, l_acc = 0.f;
+  f32x4_t o[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) o[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   EZ_TRACE(2);
   for (int it = 0; t0 < Lc; t0 += stride, ++it) {
     const int64_t tn = t0 + stride;
-    // ---- scores: acc[u][j] = S[head 4*lg + j][pos t0 + 16u + li]
+    // ---- S^T = K Q^T: acc[u][r] = S[head li][pos t0 + 16u + 4lg + r]
     f32x4_t acc[NSUB];
 #pragma unroll
     for (int u = 0; u < NSUB; ++u) {
       acc[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < NS; ++s)
-        acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf[s], as_bf16x8(kf[u][s]), acc[u], 0, 0, 0);
+        acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf[u][s]), qf[s], acc[u], 0, 0, 0);
     }
     if (EZ_ATTN_TRACE && it < 2) {
       if (acc[0][0] == 1.2345e-30f) a.Out[0] = 1;  // the stamp follows the MFMA results
@@ -370,119 +417,95 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
     load_k_tile<D, NSUB>(kr.at(tsn, id_n), tsn, tn, cl, li, lg, kf);  // next K while this tile finishes
     id_next = kr.page_id(tile_start(tn + stride, cl), lane);
 
-    float mx[4];
+    // ---- online softmax in the exp2 domain, one head per lane column
+    float mx = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      mx[j] = -INFINITY;
+    for (int u = 0; u < NSUB; ++u)
 #pragma unroll
-      for (int u = 0; u < NSUB; ++u) {
-        const bool ok = t0 + 16 * u + li < Lc;
-        const float sv = ok ? acc[u][j] * sl2 : -INFINITY;
-        acc[u][j] = sv;
-        mx[j] = fmaxf(mx[j], sv);
+      for (int r = 0; r < 4; ++r) {
+        const bool ok = t0 + 16 * u + 4 * lg + r < Lc;
+        acc[u][r] = ok ? acc[u][r] * sl2 : -INFINITY;
+        mx = fmaxf(mx, acc[u][r]);
       }
-      mx[j] = dpp_row16<true>(mx[j]);
+    mx = colgroup_max(mx);
+    const float mn = fmaxf(m_run, mx);  // finite: position t0 < Lc is in the tile
+    const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - mn);
+    m_run = mn;
+    l_acc *= alpha;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // rescale only when some running max moved
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) o[db] *= alpha;
     }
-    // ---- wave-uniform running max and rescale factors
-    float m_use[G];
+    // P^T operand: k-slot 8lg + e = position 16(e/4) + 4lg + e%4, bf16; the
+    // sum takes the rounded weights the product uses.
+    uint32_t pw[4];
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float mt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx[h & 3]), 16 * (h >> 2)));
-      const float mn = fmaxf(m_run[h], mt);
-      const float alpha = (m_run[h] == -INFINITY) ? 0.f : exp2f(m_run[h] - mn);
-      m_run[h] = mn;
-      m_use[h] = (mn == -INFINITY) ? 0.f : mn;
-      l_acc[h] *= alpha;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[h][e] *= alpha;
+    for (int q = 0; q < 4; ++q) {
+      const float p0 = __builtin_amdgcn_exp2f(acc[q >> 1][2 * (q & 1)] - mn);
+      const float p1 = __builtin_amdgcn_exp2f(acc[q >> 1][2 * (q & 1) + 1] - mn);
+      pw[q] = cvt_bf2(p0, p1);
+      l_acc += bf_lo(pw[q]) + bf_hi(pw[q]);
     }
-    // ---- P = exp2(S - m) into LDS as Ps[pos][head]
-    if (lg < GP / 4) {
+    const bf16x8_t pb = as_bf16x8(make_uint4(pw[0], pw[1], pw[2], pw[3]));
+
+    // ---- O^T += V^T P^T: this tile's V from its registers into the slab
+    // (the previous tile's reads of it have completed), then read transposed
 #pragma unroll
-      for (int u = 0; u < NSUB; ++u) {
-        float pv[4];
+    for (int i = 0; i < VI; ++i) *reinterpret_cast<uint4*>(slab + (i * kWave + lane) * 8) = vn[i];
+    asm volatile("" ::: "memory");  // the stores stay ahead of the transposing reads
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int h = 4 * lg + j;
-          float mu = m_use[j < G ? j : 0];
-          if constexpr (G > 4) mu = (lg == 1) ? m_use[4 + j] : mu;
-          pv[j] = (h < G) ? exp2f(acc[u][j] - mu) : 0.f;
-        }
-        *reinterpret_cast<float4*>(&Ps[wave][16 * u + li][4 * lg]) = make_float4(pv[0], pv[1], pv[2], pv[3]);
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // ---- O += P . V
+    for (int q = 0; q < NDB / 4; ++q) {
+      i32x2_t vt[8];
+      vt_read4<16 * D * 2>(&vaddr[4 * q], vt);
 #pragma unroll
-    for (int j = 0; j < NPV; ++j) {
-      float pr[GP];
-#pragma unroll
-      for (int q4 = 0; q4 < GP / 4; ++q4) {
-        const float4 t = *reinterpret_cast<const float4*>(&Ps[wave][rs + RPI * j][4 * q4]);
-        pr[4 * q4 + 0] = t.x; pr[4 * q4 + 1] = t.y; pr[4 * q4 + 2] = t.z; pr[4 * q4 + 3] = t.w;
-      }
-      float v[8];
-      unpack8(vf[j], v);
-      if (t0 + rs + RPI * j >= Lc) {  // masked row: its cache bytes may be anything
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = 0.f;
-      }
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        l_acc[h] += pr[h];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[h][e] = fmaf(pr[h], v[e], o[h][e]);
+      for (int k = 0; k < 4; ++k) {
+        const bf16x8_t va = __builtin_bit_cast(bf16x8_t, (u32x4_t){uint32_t(vt[2 * k][0]), uint32_t(vt[2 * k][1]),
+                                                                   uint32_t(vt[2 * k + 1][0]), uint32_t(vt[2 * k + 1][1])});
+        o[4 * q + k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, o[4 * q + k], 0, 0, 0);
       }
     }
-    load_v_tile<D, NPV>(vr.at(tsn, id_n), tsn, tn, cl, dc, rs, vf);  // next V
-    __builtin_amdgcn_wave_barrier();
+    // next V (unconditional like the K loads: past the end every row clamps
+    // to the last live row)
+    load_v_regs<D>(vr.at(tsn, id_n), tsn, tn, cl, lane, vn);
   }
 
+  // l: the four lanes of a head column hold its partial sums.
+  l_acc = rowgroup_sum<16>(l_acc);
   if constexpr (LAYER) {
     // The decoded token as one more row of wave 0 of split 0: s_h = q_h . k
     // (fp32 over the bf16 values the cache holds), then the same online
-    // update; P and V enter through the row-group-0 lanes only (the row
-    // groups are summed below).
+    // update in fp32, lane column h.
     if (split == 0 && wave == 0 && L > 0) {
+      float sv = -INFINITY;
 #pragma unroll
       for (int h = 0; h < G; ++h) {
         float d = 0.f;
         for (int i = lane; i < D; i += kWave) d = fmaf(bf2f(Qs[h][i]), bf2f(Kn[i]), d);
-        const float sv = wave_reduce_uniform<false>(d) * sl2;
-        const float mn = fmaxf(m_run[h], sv);
-        const float alpha = (m_run[h] == -INFINITY) ? 0.f : exp2f(m_run[h] - mn);
-        const float pv = rs == 0 ? exp2f(sv - mn) : 0.f;
-        m_run[h] = mn;
-        l_acc[h] = fmaf(l_acc[h], alpha, pv);
+        const float sh = wave_reduce_uniform<false>(d) * sl2;
+        sv = li == h ? sh : sv;
+      }
+      if (li < G) {
+        const float mn = fmaxf(m_run, sv);
+        const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - mn);
+        const float pv = __builtin_amdgcn_exp2f(sv - mn);
+        m_run = mn;
+        l_acc = fmaf(l_acc, alpha, pv);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[h][e] = fmaf(o[h][e], alpha, pv * bf2f(Vn[dc * 8 + e]));
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[db][r] = fmaf(o[db][r], alpha, pv * bf2f(Vn[16 * db + 4 * lg + r]));
       }
     }
   }
 
   EZ_TRACE(5);
-  // ---- merge the row groups of the wave (lanes with equal dc): VALU lane
-  // swaps, no LDS round trips
+  if (li < G) {
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    l_acc[h] = rowgroup_sum<CPR>(l_acc[h]);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[h][e] = rowgroup_sum<CPR>(o[h][e]);
-  }
-  if (rs == 0) {
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      *reinterpret_cast<float4*>(&Os[wave][h][dc * 8]) = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
-      *reinterpret_cast<float4*>(&Os[wave][h][dc * 8 + 4]) = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
-    }
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      Ms[wave][h] = m_run[h];
-      Ls[wave][h] = l_acc[h];
+    for (int db = 0; db < NDB; ++db)
+      *reinterpret_cast<float4*>(&Os[wave][li][16 * db + 4 * lg]) = make_float4(o[db][0], o[db][1], o[db][2], o[db][3]);
+    if (lg == 0) {
+      Ms[wave][li] = m_run;
+      Ls[wave][li] = l_acc;
     }
   }
   __syncthreads();

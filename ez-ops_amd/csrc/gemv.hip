@@ -188,12 +188,6 @@ constexpr int kMfmaSteps = kMfmaKC / 32;         // MFMA k-steps per chunk
 constexpr int kMfmaSlices = 16 * kMfmaKC / 512;  // 1 KiB DMA slices per 16-row tile and chunk
 
 
-// s_waitcnt with vmcnt = N and the other counters unconstrained (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 typedef unsigned int u32x4v_t __attribute__((ext_vector_type(4)));
 

@@ -36,13 +36,6 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-// Two fp32 -> packed bf16 in one hardware convert (round to nearest even).
-__device__ __forceinline__ uint32_t cvt_bf2(float lo, float hi) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
-}
-
 // Value of the other lane half (lane l ^ 32) combined with this lane's.
 __device__ __forceinline__ float halves_max(float v) {
   const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
