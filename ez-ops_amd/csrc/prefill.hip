@@ -7,7 +7,8 @@
 // C[8(r/4) + 4h + r%4][j]):
 //   S^T = K Q^T   A = 32 keys x 16 dims of K (LDS, XOR-swizzled rows),
 //                 B = Q^T (registers, loaded once), C = S^T[key][query]
-//   O^T = V^T P^T A = V^T (LDS, stored transposed), B = P^T straight from the
+//   O^T = V^T P^T A = V^T (row-major LDS tile, read by transposing
+//                 ds_read_b64_tr_b16), B = P^T straight from the
 //                 S^T registers: the k slots 8h..8h+7 of a 16-key step are
 //                 keys 4h..4h+3 and 8+4h..8+4h+3 of it, the same slot order
 //                 in A and B, so P never leaves the lane.
@@ -31,7 +32,6 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kPD = 128;            // head dim
 constexpr int kPW = 4;              // waves per block
 constexpr int kBK = 64;             // keys per tile
-constexpr int kVtStride = kBK + 4;  // transposed V row stride (elements): 8-byte aligned, padded
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -81,17 +81,27 @@ __device__ __forceinline__ void lds_read8(const uint32_t (&addr)[8], u32x4v_t (&
         "v"(addr[7]));
 }
 static_assert(kPD / 16 == 8, "lds_read8 reads the 8 k-steps of a 128-dim key row");
-// Reads 4 V^T fragments (two 8-byte halves 16 bytes apart each) from LDS
-// and waits for them; an asm block for the same reason as lds_read8.
-__device__ __forceinline__ void lds_read_vt4(const uint32_t (&addr)[4], u32x4v_t (&r)[4]) {
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
+// The 4 V^T operands (dimension blocks d = 0..3) of one 16-key step by
+// transposing LDS reads (ds_read_b64_tr_b16: in each 16-lane group, lane m
+// receives element m%4 of the 8-byte rows that lanes m/4, 4 + m/4, 8 + m/4
+// and 12 + m/4 address): r[2d] from addr[d] + OFF, r[2d+1] 8 key rows
+// further.  One asm block with its own wait, for the same reason as
+// lds_read8.
+template <int OFF>
+__device__ __forceinline__ void lds_read_vt4(const uint32_t (&addr)[4], i32x2_t (&r)[8]) {
   asm volatile(
-      "ds_read2_b64 %0, %4 offset1:2\n\t"
-      "ds_read2_b64 %1, %5 offset1:2\n\t"
-      "ds_read2_b64 %2, %6 offset1:2\n\t"
-      "ds_read2_b64 %3, %7 offset1:2\n\t"
+      "ds_read_b64_tr_b16 %0, %8 offset:%12\n\t"
+      "ds_read_b64_tr_b16 %1, %8 offset:%13\n\t"
+      "ds_read_b64_tr_b16 %2, %9 offset:%12\n\t"
+      "ds_read_b64_tr_b16 %3, %9 offset:%13\n\t"
+      "ds_read_b64_tr_b16 %4, %10 offset:%12\n\t"
+      "ds_read_b64_tr_b16 %5, %10 offset:%13\n\t"
+      "ds_read_b64_tr_b16 %6, %11 offset:%12\n\t"
+      "ds_read_b64_tr_b16 %7, %11 offset:%13\n\t"
       "s_waitcnt lgkmcnt(0)"
-      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
-      : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]));
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+      : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "i"(OFF), "i"(OFF + 8 * kPD * 2));
 }
 static_assert(kPD / 32 == 4, "lds_read_vt4 reads the 4 dimension blocks of a 128-dim head");
 
@@ -106,7 +116,7 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
   constexpr int NHB = G / HPB;  // head groups per kv head
   constexpr int BQ = 32 * (kPW / HPB);
   __shared__ __align__(16) uint16_t Ks[2][kBK * kPD];        // [key][16B chunk ^ (key & 15)]
-  __shared__ __align__(16) uint16_t Vt[2][kPD * kVtStride];  // [dim][key]
+  __shared__ __align__(16) uint16_t Vs[2][kBK * kPD];        // [key][16B chunk ^ 2(key & 7)]
 
   const int per_q = int(a.B * a.Hkv) * NHB;
   const int qt = ntq - 1 - int(blockIdx.x) / per_q;  // longest (last) query tiles first
@@ -149,17 +159,16 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
 
   // staging: K chunks id = tid + 256c -> key id/16, chunk id%16; V: keys
   // 4*vm .. 4*vm+3 (vm = tid/16), dims 8*vc .. 8*vc+7 (vc = tid%16)
-  uint4 vr[4];
-  const int vm = tid >> 4, vc = tid & 15;
   // contiguous cache: the (sequence, kv head) slabs, rows addressed in 32 bits
   const uint16_t* kslab = a.K + (int64_t(b) * a.Hkv + kvh) * a.S * kPD;
   const uint16_t* vslab = a.V + (int64_t(b) * a.Hkv + kvh) * a.S * kPD;
   const int kend32 = int(kend);
-  // K goes straight to LDS (global_load_lds_dwordx4): load c of wave w fills
-  // LDS chunks 256c + 64w .. +63, one per lane, so lane tid writes chunk
-  // p = 256c + tid = (key p/16, swizzled slot p%16) and reads the global
-  // chunk (p%16) ^ (key & 15) of that key.  V is staged in registers and
-  // transposed on the LDS store.
+  // K and V go straight to LDS (global_load_lds_dwordx4): load c of wave w
+  // fills LDS chunks 256c + 64w .. +63, one per lane, so lane tid writes
+  // chunk p = 256c + tid = (key p/16, slot p%16) and reads the global chunk
+  // slot ^ (key & 15) of K (conflict-free 16-byte reads of the S operand)
+  // and slot ^ 2(key & 7) of V (conflict-free transposing reads of the V^T
+  // operand, 4 keys x 32 bytes per 16 lanes).
   auto load_tile = [&](int64_t k0, int nb) {
     const int k032 = int(k0);
 #pragma unroll
@@ -167,35 +176,24 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
       const int id = tid + c * kPW * kWave;
       const int r = id >> 4;
       const int row = min(k032 + r, kend32 - 1);
-      const int cc = (id & 15) ^ (r & 15);
-      const int vrow = min(k032 + 4 * vm + c, kend32 - 1);
-      const uint16_t* kp;
+      const int kc = (id & 15) ^ (r & 15), vc = (id & 15) ^ (2 * (r & 7));
+      const uint16_t *kp, *vp;
       if constexpr (PAGED) {
-        kp = cache_row<PAGED>(a, a.K, b, kvh, row) + cc * 8;
-        vr[c] = *reinterpret_cast<const uint4*>(cache_row<PAGED>(a, a.V, b, kvh, vrow) + vc * 8);
+        kp = cache_row<PAGED>(a, a.K, b, kvh, row) + kc * 8;
+        vp = cache_row<PAGED>(a, a.V, b, kvh, row) + vc * 8;
       } else {
-        kp = kslab + uint32_t(row * kPD + cc * 8);
-        vr[c] = *reinterpret_cast<const uint4*>(vslab + uint32_t(vrow * kPD + vc * 8));
+        kp = kslab + uint32_t(row * kPD + kc * 8);
+        vp = vslab + uint32_t(row * kPD + vc * 8);
       }
+      const int slot = (c * kPW + wave) * kWave * 8;
       __builtin_amdgcn_global_load_lds(static_cast<const void*>(kp),
-                                       (__attribute__((address_space(3))) void*)(&Ks[nb][(c * kPW + wave) * kWave * 8]),
-                                       16, 0, 0);
+                                       (__attribute__((address_space(3))) void*)(&Ks[nb][slot]), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(vp),
+                                       (__attribute__((address_space(3))) void*)(&Vs[nb][slot]), 16, 0, 0);
     }
   };
-  auto store_tile = [&](int buf) {
-    // word w of a 16-byte chunk, by field
-    auto word = [](const uint4& v, int w) { return w == 0 ? v.x : w == 1 ? v.y : w == 2 ? v.z : v.w; };
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int sh = (e & 1) * 16;
-      const uint32_t k0v = (word(vr[0], e >> 1) >> sh) & 0xffffu, k1v = (word(vr[1], e >> 1) >> sh) & 0xffffu;
-      const uint32_t k2v = (word(vr[2], e >> 1) >> sh) & 0xffffu, k3v = (word(vr[3], e >> 1) >> sh) & 0xffffu;
-      *reinterpret_cast<uint2*>(&Vt[buf][(vc * 8 + e) * kVtStride + 4 * vm]) =
-          make_uint2(k0v | (k1v << 16), k2v | (k3v << 16));
-    }
-    // the K DMA into this buffer has landed before the barrier that follows
-    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
-  };
+  // the DMA into a buffer has landed before the barrier that follows
+  auto store_tile = [&](int) { wait_vm<0>(); };
   load_tile(0, 0);
   store_tile(0);
   __syncthreads();
@@ -209,8 +207,21 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
       f32x16_t st[kBK / 32];
       const uint32_t ks_base =
           uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint16_t*)(&Ks[buf][0])));
-      const uint32_t vt_base =
-          uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint16_t*)(&Vt[buf][0])));
+      // V^T operand addresses: lane (i = 16(g%2) + m of 16-lane group g, half
+      // h) reads key row 4h + m/4 (+ 16-key step, + 8 for the second half),
+      // dims 32d + i - m%4 + 4(m%4) .. +3 = 32d + 16(g%2) + 4(m%4) .. +3.
+      uint32_t vaddr[kPD / 32];
+      {
+        const uint32_t vs_base =
+            uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint16_t*)(&Vs[buf][0])));
+        const int mm = lane & 15, g1 = (lane >> 4) & 1;
+        const int vrow = 4 * h + (mm >> 2);
+#pragma unroll
+        for (int d = 0; d < kPD / 32; ++d) {
+          const int ch = 4 * d + 2 * g1 + ((mm & 3) >> 1);
+          vaddr[d] = vs_base + uint32_t(vrow * kPD * 2 + ((ch ^ (2 * (vrow & 7))) * 16) + (mm & 1) * 8);
+        }
+      }
       uint32_t kaddr[kPD / 16];
 #pragma unroll
       for (int kk = 0; kk < kBK / 32; ++kk) {
@@ -263,15 +274,19 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
             w[q] = cvt_bf2(p0, p1);
           }
           const bf16x8_t pb = as_bf16x8(make_uint4(w[0], w[1], w[2], w[3]));
-          const int kc = 32 * kk + 16 * u + 4 * h;
-          uint32_t vaddr[kPD / 32];
+          // keys 32kk + 16u + 4h + 0..3 and + 8..11 of dims 32d + j
+          i32x2_t vf[2 * (kPD / 32)];
+          if (kk == 0 && u == 0) lds_read_vt4<0>(vaddr, vf);
+          else if (kk == 0) lds_read_vt4<16 * kPD * 2>(vaddr, vf);
+          else if (u == 0) lds_read_vt4<32 * kPD * 2>(vaddr, vf);
+          else lds_read_vt4<48 * kPD * 2>(vaddr, vf);
 #pragma unroll
-          for (int d = 0; d < kPD / 32; ++d) vaddr[d] = vt_base + uint32_t((32 * d + j) * kVtStride + kc) * 2;
-          u32x4v_t vf[kPD / 32];
-          lds_read_vt4(vaddr, vf);  // keys kc..kc+3 and kc+8..kc+11 of dims 32d + j
-#pragma unroll
-          for (int d = 0; d < kPD / 32; ++d)
-            o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vf[d]), pb, o[d], 0, 0, 0);
+          for (int d = 0; d < kPD / 32; ++d) {
+            const bf16x8_t va = __builtin_bit_cast(
+                bf16x8_t, (u32x4v_t){uint32_t(vf[2 * d][0]), uint32_t(vf[2 * d][1]), uint32_t(vf[2 * d + 1][0]),
+                                     uint32_t(vf[2 * d + 1][1])});
+            o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, o[d], 0, 0, 0);
+          }
         }
       }
     }
