@@ -116,7 +116,7 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
   constexpr int NHB = G / HPB;  // head groups per kv head
   constexpr int BQ = 32 * (kPW / HPB);
   __shared__ __align__(16) uint16_t Ks[2][kBK * kPD];        // [key][16B chunk ^ (key & 15)]
-  __shared__ __align__(16) uint16_t Vs[2][kBK * kPD];        // [key][16B chunk ^ 2(key & 7)]
+  __shared__ __align__(16) uint16_t Vs[2][kBK * kPD];        // [key][16B chunk ^ 4(key & 3)]
 
   const int per_q = int(a.B * a.Hkv) * NHB;
   const int qt = ntq - 1 - int(blockIdx.x) / per_q;  // longest (last) query tiles first
@@ -167,8 +167,9 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
   // fills LDS chunks 256c + 64w .. +63, one per lane, so lane tid writes
   // chunk p = 256c + tid = (key p/16, slot p%16) and reads the global chunk
   // slot ^ (key & 15) of K (conflict-free 16-byte reads of the S operand)
-  // and slot ^ 2(key & 7) of V (conflict-free transposing reads of the V^T
-  // operand, 4 keys x 32 bytes per 16 lanes).
+  // and slot ^ 4(key & 3) of V: the transposing reads of the V^T operand
+  // take 4 keys x 64 bytes per 32 lanes, each key in its own 64-byte bank
+  // block.
   auto load_tile = [&](int64_t k0, int nb) {
     const int k032 = int(k0);
 #pragma unroll
@@ -176,7 +177,7 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
       const int id = tid + c * kPW * kWave;
       const int r = id >> 4;
       const int row = min(k032 + r, kend32 - 1);
-      const int kc = (id & 15) ^ (r & 15), vc = (id & 15) ^ (2 * (r & 7));
+      const int kc = (id & 15) ^ (r & 15), vc = (id & 15) ^ (4 * (r & 3));
       const uint16_t *kp, *vp;
       if constexpr (PAGED) {
         kp = cache_row<PAGED>(a, a.K, b, kvh, row) + kc * 8;
@@ -219,7 +220,7 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
 #pragma unroll
         for (int d = 0; d < kPD / 32; ++d) {
           const int ch = 4 * d + 2 * g1 + ((mm & 3) >> 1);
-          vaddr[d] = vs_base + uint32_t(vrow * kPD * 2 + ((ch ^ (2 * (vrow & 7))) * 16) + (mm & 1) * 8);
+          vaddr[d] = vs_base + uint32_t(vrow * kPD * 2 + ((ch ^ (4 * (vrow & 3))) * 16) + (mm & 1) * 8);
         }
       }
       uint32_t kaddr[kPD / 16];
