@@ -449,7 +449,15 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
     const bf16x8_t pb = as_bf16x8(make_uint4(pw[0], pw[1], pw[2], pw[3]));
 
     // ---- O^T += V^T P^T: this tile's V from its registers into the slab
-    // (the previous tile's reads of it have completed), then read transposed
+    // (the previous tile's reads of it have completed), then read transposed.
+    // Rows at or past the length get P = 0 but must not hold non-finite
+    // values (0 * NaN): a wave's first tile is requested before the length
+    // is known and may read such rows; they are zeroed here.
+    if (t0 + kTile > Lc) {
+#pragma unroll
+      for (int i = 0; i < VI; ++i)
+        if (t0 + i * (kWave / (D / 8)) + lane / (D / 8) >= Lc) vn[i] = make_uint4(0, 0, 0, 0);
+    }
 #pragma unroll
     for (int i = 0; i < VI; ++i) *reinterpret_cast<uint4*>(slab + (i * kWave + lane) * 8) = vn[i];
     asm volatile("" ::: "memory");  // the stores stay ahead of the transposing reads

@@ -135,6 +135,30 @@ def test_attn_decode(B, H, Hkv, S, D, ragged):
     assert torch.equal(out, out2)
 
 
+@pytest.mark.parametrize("H,Hkv,D", [(32, 8, 128), (16, 16, 64), (32, 4, 128)])
+def test_attn_decode_tile_residues_and_nonfinite_tail(H, Hkv, D):
+    """Every length residue modulo the 32-position tile (1, 31, 33, ...), with
+    NaN / Inf in every cache row at or past the length: those rows are never
+    read (tile rows past the length are clamped to the last live row), so the
+    result matches the oracle over the live rows."""
+    B, S = 8, 160
+    op = AttnDecodeOp(B, H, S, D, backend="hip", num_kv_heads=Hkv)
+    torch.manual_seed(29)
+    Q, K, V = op.gen_data()
+    nK, nV = n(K).copy(), n(V).copy()
+    for start in (1, 9, 17, 25):
+        lens = torch.tensor([start + 4 * b for b in range(B)], dtype=torch.int32)
+        lens[-1] = 1
+        Kg, Vg = K.clone(), V.clone()
+        for b, L in enumerate(lens.tolist()):
+            Kg[b, :, L:] = float("nan")
+            Vg[b, :, L:] = float("inf")
+        out = op(Q, Kg, Vg, lens.to(DEV))
+        ref = oracle.attn_decode(n(Q)[:, :, 0], nK, nV, lens.numpy().astype(np.int64))
+        assert torch.isfinite(out).all()
+        np.testing.assert_allclose(n(out)[:, :, 0], ref, **BF_TOL)
+
+
 @pytest.mark.parametrize("B,S,bound", [(1, 16384, "max"), (3, 4096, "max"), (4, 8192, "cut"), (2, 3000, "over")])
 def test_attn_decode_max_kv_len(B, S, bound):
     """max_kv_len plans the grid on the caller's length bound; lengths above

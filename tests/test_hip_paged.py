@@ -129,3 +129,24 @@ def test_paged_attn_deterministic_and_inputs_read_only():
     b = op(*data, max_kv_len=2048)
     assert torch.equal(a, b)
     assert all(torch.equal(x, y) for x, y in zip(data, before))
+
+
+def test_paged_nonfinite_rows_past_lengths():
+    """Pool rows that hold no live position (past a sequence's length, or
+    pages no table entry reaches) may hold NaN / Inf: they are never read."""
+    B, H, Hkv, D, P, M, NP = 4, 32, 8, 128, 32, 8, 40
+    torch.manual_seed(17)
+    op = PagedAttnDecodeOp(B, H, Hkv, D, page_size=P, max_pages=M, num_pages=NP, backend="hip")
+    Q, Kp, Vp, bt, _ = op.gen_data()
+    lens = torch.tensor([M * P, 33, 1, 95], dtype=torch.int32, device=DEV)
+    ref = oracle.paged_attn_decode(n(Q)[:, :, 0], n(Kp), n(Vp), bt.cpu().numpy(), n(lens).astype(np.int64), P)
+    live = torch.zeros(NP, P, dtype=torch.bool, device=DEV)
+    for b, L in enumerate(lens.tolist()):
+        for t in range(L):
+            live[int(bt[b, t // P]), t % P] = True
+    Kg, Vg = Kp.clone(), Vp.clone()
+    Kg.transpose(1, 2)[~live] = float("nan")
+    Vg.transpose(1, 2)[~live] = float("inf")
+    out = op(Q, Kg, Vg, bt, lens)
+    assert torch.isfinite(out).all()
+    np.testing.assert_allclose(n(out)[:, :, 0], ref, **BF_TOL)
