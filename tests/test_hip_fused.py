@@ -136,6 +136,27 @@ def test_qwen3_layer_repeated_calls():
         assert op.check(out, torch.from_numpy(ref).to(out.device)), it
 
 
+@pytest.mark.parametrize("batch,kv_lens", [(1, [3000]), (4, [1, 31, 33, 2049])])
+def test_qwen3_layer_ignores_rows_past_lengths(batch, kv_lens):
+    """Cache rows past each sequence's length (the decoded token goes to row
+    len - 1) are never read: NaN there leaves the output and the written
+    rows bit-identical to a run over finite values."""
+    torch.manual_seed(13)
+    op = Qwen3DenseDecodeOp(batch, 4096, backend="hip", kv_lens=kv_lens, norm_weights=True, rope_theta=1e6,
+                            **QWEN3_8B, num_kv_heads=8)
+    data = list(op.gen_data())
+    ref_K, ref_V = data[1].clone(), data[2].clone()
+    out_ref = op(data[0], ref_K, ref_V, *data[3:])
+    K, V = data[1].clone(), data[2].clone()
+    for b, L in enumerate(kv_lens):
+        K[b, :, L:] = float("nan")
+        V[b, :, L:] = float("inf")
+    out = op(data[0], K, V, *data[3:])
+    assert torch.equal(out, out_ref)
+    for b, L in enumerate(kv_lens):
+        assert torch.equal(K[b, :, :L], ref_K[b, :, :L]) and torch.equal(V[b, :, :L], ref_V[b, :, :L])
+
+
 @pytest.mark.parametrize("batch", [1, 16])
 def test_qwen3_layer_graph_replays(batch):
     """The layer captured once in a HIP graph and replayed: every replay equals
