@@ -193,10 +193,8 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
                                        (__attribute__((address_space(3))) void*)(&Vs[nb][slot]), 16, 0, 0);
     }
   };
-  // the DMA into a buffer has landed before the barrier that follows
-  auto store_tile = [&](int) { wait_vm<0>(); };
   load_tile(0, 0);
-  store_tile(0);
+  wait_vm<0>();  // the first tile has landed before the barrier
   __syncthreads();
 
   int buf = 0;
@@ -291,7 +289,7 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
         }
       }
     }
-    if (more) store_tile(buf ^ 1);
+    if (more) wait_vm<0>();  // the next tile's DMA has landed before the barrier
     __syncthreads();
   }
 
