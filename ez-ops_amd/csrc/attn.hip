@@ -589,8 +589,12 @@ struct SplitPlan {
 
 // Splits per (b, kv head), planned on the length bound Lh: enough blocks to
 // keep every CU busy, at least one tile per wave at length Lh, and at most
-// kMaxSplits partials per merge.
-SplitPlan plan_splits(int64_t B, int64_t Hkv, int64_t Lh, int64_t G) {
+// kMaxSplits partials per merge.  balance: then the fewest splits that keep
+// the same maximum of tiles per wave (B=1 at 9291 positions: 19 splits, 2
+// tiles on the busiest wave as with 32, and a cheaper merge).  The
+// unbalanced plan bounds the balanced one for every Lh up to its own, so the
+// workspace is sized with it.
+SplitPlan plan_splits(int64_t B, int64_t Hkv, int64_t Lh, int64_t G, bool balance = true) {
   const int64_t units = B * Hkv;
   const int64_t cus = num_cus();
   // 8-wave blocks for few units; group 8 keeps 4 waves (its accumulators need
@@ -602,6 +606,12 @@ SplitPlan plan_splits(int64_t B, int64_t Hkv, int64_t Lh, int64_t G) {
   if (ns > max_ns) ns = max_ns;
   if (ns > kMaxSplits) ns = kMaxSplits;
   if (ns < 1) ns = 1;
+  if (balance) {
+    const int64_t tiles = (Lh + kTile - 1) / kTile;
+    const int64_t per_wave = (tiles + ns * waves - 1) / (ns * waves);  // tiles on the busiest wave
+    if (per_wave > 0) ns = (tiles + per_wave * waves - 1) / (per_wave * waves);
+    if (ns < 1) ns = 1;
+  }
   return {waves, int(ns)};
 }
 
@@ -631,7 +641,7 @@ void launch_d(const AttnArgs& a, const SplitPlan& pl, float* opart, float* ml, i
 // The workspace is planned on the capacity S, an upper bound for every Lh.
 size_t attn_workspace_size(int64_t B, int64_t H, int64_t Hkv, int64_t S, int64_t D) {
   if (B < 1 || H < 1 || Hkv < 1 || S < 1 || D < 1) return 0;
-  const SplitPlan pl = plan_splits(B, Hkv, S, H / Hkv);
+  const SplitPlan pl = plan_splits(B, Hkv, S, H / Hkv, false);
   return align256(size_t(B * H * pl.nsplit * D) * 4) + align256(size_t(B * H * pl.nsplit * 2) * 4);
 }
 
