@@ -257,7 +257,10 @@ int ezops_qwen3_decode_step_bf16(const ezops_qwen3_layer* layers, int64_t n_laye
  * ezops_qwen3_dense_decode_paged_bf16.  max_q_len: host bound on the
  * per-sequence token counts.  D = 128, IS % 8 == 0.  GEMMs run through
  * hipBLASLt (a shape's first call sets up its algorithm on the host; run it
- * eagerly once before capturing a graph).
+ * eagerly once before capturing a graph).  The algorithm is the fastest of
+ * the heuristic's candidates timed on that first call, so two processes may
+ * keep different ones and agree only to bf16 rounding; within a process the
+ * results are deterministic.
  * No counterpart in the reference (decode only,
  * ezops/ops/qwen3_dense_decode.py:9-176): the step that fills the cache the
  * decode layer reads. */
