@@ -75,10 +75,30 @@ def build(jobs: int | None = None, verbose: bool = True, extra_flags: tuple = ()
     return lib
 
 
+KAT_SRC = PKG_ROOT.parent / "tests" / "kat_c_abi.cpp"
+KAT_BIN = LIB.parent / "ezops_kat_c_abi"
+
+
+def build_kat(verbose: bool = True) -> Path:
+    """The C++ known-answer program of the C ABI (tests/kat_c_abi.cpp), linked
+    against the in-tree library through an $ORIGIN rpath."""
+    tmp = KAT_BIN.with_suffix(".tmp")
+    cmd = [hipcc(), "-O2", "-std=c++17", str(KAT_SRC), f"-L{LIB.parent}", "-lezops_hip",
+           "-Wl,-rpath,$ORIGIN", "-o", str(tmp)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"KAT build failed: {' '.join(cmd)}\n{r.stdout}{r.stderr}")
+    os.replace(tmp, KAT_BIN)
+    if verbose:
+        print(f"built {KAT_BIN}")
+    return KAT_BIN
+
+
 def build_all(jobs: int | None = None, verbose: bool = True) -> None:
-    """The production library and its profiling variant."""
+    """The production library, its profiling variant and the C ABI KAT program."""
     build(jobs, verbose)
     build(jobs, verbose, extra_flags=("-DEZ_PROFILE=1",), lib=PROF_LIB, build_dir=BUILD / "prof")
+    build_kat(verbose)
 
 
 if __name__ == "__main__":
