@@ -7,6 +7,7 @@
 //   attn:     q = 0 (uniform softmax over the live rows), V rows of 3s, 6s,
 //             9s: the output is 6 everywhere (exact in bf16), with a length
 //             of 3 inside a larger cache whose other rows hold 1000
+//   prefill:  q = 0 over 16 new tokens: token i averages V rows 0..i
 //   rmsnorm:  rows of +-2: x * rsqrt(4 + eps) = +-1 within 1e-6
 //   errors:   N = 0 is rejected with EZOPS_EINVAL and a message
 #include <hip/hip_runtime.h>
@@ -105,6 +106,34 @@ void kat_attn() {
   (void)hipFree(dws);
 }
 
+void kat_prefill_attn() {
+  // q = 0: token i attends keys 0..i uniformly; V row r holds 3(r + 1), so
+  // every output of token i is 3(i + 2) / 2 (exact in bf16 for i < 16).
+  const int64_t B = 1, T = 16, H = 4, Hkv = 1, S = 16, D = 128;
+  std::vector<uint16_t> Q(T * H * D, bf(0.f)), K(B * Hkv * S * D), V(B * Hkv * S * D), O(T * H * D, 0);
+  for (int64_t r = 0; r < S; ++r)
+    for (int64_t d = 0; d < D; ++d) {
+      K[r * D + d] = bf(float((r + d) % 7) - 3.f);
+      V[r * D + d] = bf(float(3 * (r + 1)));
+    }
+  const std::vector<int32_t> cu{0, int32_t(T)};
+  uint16_t *dQ = dev(Q), *dK = dev(K), *dV = dev(V), *dO = dev(O);
+  int32_t* dcu = dev(cu);
+  const int rc = ezops_prefill_attn_bf16(dQ, dK, dV, dO, dcu, nullptr, B, T, H, Hkv, S, D, T, nullptr, 0, 0, 0.f,
+                                         nullptr);
+  check(rc == 0 && hipDeviceSynchronize() == hipSuccess, "prefill_attn returns 0");
+  const auto out = host(dO, size_t(T * H * D));
+  bool ok = out.size() == size_t(T * H * D);
+  for (int64_t i = 0; ok && i < T; ++i)
+    for (int64_t j = 0; ok && j < H * D; ++j) ok = fb(out[i * H * D + j]) == 1.5f * float(i + 2);
+  check(ok, "prefill_attn: token i averages V rows 0..i, 3(i + 2) / 2, exact");
+  (void)hipFree(dQ);
+  (void)hipFree(dK);
+  (void)hipFree(dV);
+  (void)hipFree(dO);
+  (void)hipFree(dcu);
+}
+
 void kat_rmsnorm() {
   const int64_t rows = 3, dim = 100;
   std::vector<float> X(rows * dim), Out(rows * dim, 0.f);
@@ -137,6 +166,7 @@ int main() {
   std::printf("abi version %d\n", ezops_hip_abi_version());
   kat_gemv();
   kat_attn();
+  kat_prefill_attn();
   kat_rmsnorm();
   kat_errors();
   std::printf(failures ? "KAT FAILED (%d)\n" : "KAT OK\n", failures);

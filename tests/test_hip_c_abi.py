@@ -1,7 +1,9 @@
 """The C ABI from C++ with no Python in the loop (GPU): tests/kat_c_abi.cpp,
 built next to the library by ez-ops_amd/build.py, runs known-answer cases
 whose results are exact (GEMV of small integers, decode attention with a
-uniform softmax over the live rows of a larger cache, RMSNorm of +-2 rows)
+uniform softmax over the live rows of a larger cache, causal prefill
+attention with a uniform softmax over each token's prefix, RMSNorm of +-2
+rows)
 and the EZOPS_EINVAL error path, as a child process."""
 
 import subprocess
