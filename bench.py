@@ -375,7 +375,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the decode ops run on one MI355X; see the sharding notes in DESIGN.md).", file=sys.stderr)
+              "(the decode ops run on one MI355X; multi-GPU sharding is designed, not built).", file=sys.stderr)
         return 2
 
     import numpy as np
