@@ -1,14 +1,17 @@
 """MI355X benchmark of the ez-ops decode hot path on the HIP backend.
 
 Headline (BASELINE.json metric): sol-score = achieved / measured-peak HBM
-bandwidth, and microseconds per Qwen3-8B dense decode layer at batch 1
+bandwidth (the peak is the best sustained rate measured in the same run: the
+non-temporal read probe, or a kernel of the run if one reads faster), and
+microseconds per Qwen3-8B dense decode layer at batch 1
 (config L: hidden 4096, 32/8 heads x 128, intermediate 12288, RMSNorm eps
 1e-6 with weights, RoPE theta 1e6, KV length ~ U[1024, 16384], seed 4).
 
 One "step" = one decode-layer forward (5 kernels, replayed from a HIP graph)
 with every input already in HBM.  Between steps a 1 GiB read evicts L2 and
 the 256 MB MALL (outside the timed events), so each step streams its
-~424 MB from HBM.  The per-op table covers the other BASELINE configs.
+~424 MB from HBM.  The per-op table covers the other BASELINE configs; the
+CPU baseline runs the reference's torch formulas (backend "ref") on the host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-ops] [--no-cpu]
 Prints ONE JSON line.
@@ -97,16 +100,11 @@ def hbm_peak(torch, _hip) -> dict:
 
 
 # --------------------------------------------------------------- workloads
-def layer_workload(torch, batch: int, seed: int = 4):
-    from ezops import Qwen3DenseDecodeOp
+def layer_workload(torch, batch: int):
+    """Config L at ``batch``: (op, data, lens), inputs drawn on the GPU with seed 4."""
+    from ezops import workloads
 
-    gen = torch.Generator().manual_seed(seed)
-    lens = torch.randint(1024, SEQ_MAX + 1, (batch,), generator=gen).tolist()
-    op = Qwen3DenseDecodeOp(batch, SEQ_MAX, backend="hip", kv_lens=lens, norm_weights=True, rope_theta=1e6,
-                            **QWEN3_8B)
-    torch.manual_seed(seed)
-    data = op.gen_data("cuda")
-    return op, data, lens
+    return workloads.config_l(batch, "cuda")
 
 
 def layer_bytes(batch: int, lens) -> int:
@@ -191,39 +189,97 @@ def prefill(torch, flush) -> dict:
     return out
 
 
-def cpu_baseline(torch, op, data, lens, budget_s: float = 20.0) -> dict:
-    """The numpy oracle (fp32 BLAS restatement of the reference layer) on this host."""
-    import numpy as np
-
-    import oracle
-
-    npy = [x.float().cpu().numpy() for x in data]
-    kw = dict(kv_lens=lens, in_norm_w=npy[7], q_norm_w=npy[8], k_norm_w=npy[9], post_norm_w=npy[10],
-              cos=npy[11], sin=npy[12])
-
-    def run():
-        return oracle.qwen3_layer(npy[0], npy[1], npy[2], *npy[3:7], 32, 8, 128, **kw)[0]
-
-    t0 = time.perf_counter()
-    out = run()  # warmup
-    one = time.perf_counter() - t0
-    reps = max(3, min(15, int(budget_s / max(one, 1e-3))))
-    times = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
+def cpu_model() -> str:
     try:
-        from threadpoolctl import threadpool_info
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:
-        threads = os.cpu_count() or 1
-    med = statistics.median(times)
-    return {"out": out, "sec": med, "reps": reps, "threads": threads}
+
+def cpu_ref_baseline(torch, layer_data, lens, budget_s: float = 4.0) -> dict:
+    """The package's ``backend="ref"`` path (each op's ``_ref_forward``, the
+    reference's torch formulas) on torch CPU tensors in the reference's dtypes,
+    all host threads, 2 warm-ups then the median of >= 5 timed runs per op.
+
+    Inputs are this run's GPU tensors copied to the host, so both sides see the
+    same values.  Per op: G, N (RMSNorm / softmax / sum), A (a sample of 4 of
+    the 32 sequences, scaled x8 to the full config), F1 and F2 at batch 1, and
+    the config-L layer at the headline batch."""
+    from ezops import (AttnDecodeOp, FusedOProjFfnOp, FusedQkNormRopeOp, GemvOp, Qwen3DenseDecodeOp, ReduceOp,
+                       RmsNormOp, SoftmaxOp, workloads)
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    cpu = lambda ts: [t.cpu() for t in ts]  # noqa: E731
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        times = []
+        t_end = time.perf_counter() + budget_s
+        while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 15):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times), len(times)
+
+    ops = {}
+
+    def rec(name, fn, nbytes, scale=1, sample=None):
+        sec, reps = timed(fn)
+        us = sec * 1e6 * scale
+        ops[name] = {"us": round(us, 1), "GBps": round(nbytes / (us * 1e-6) / 1e9, 3), "reps": reps,
+                     **({"sample": sample} if sample else {})}
+        log(f"cpu ref {name}: {us:.0f} us")
+
+    x, W = cpu(workloads.config_g("cuda"))
+    g = GemvOp(4096, 4096)  # ref backend: B is [K, N]
+    Bt, C = W.T.contiguous(), torch.empty(4096, dtype=torch.bfloat16)
+    rec("gemv_4096x4096", lambda: g(x, Bt, C), 33_570_816)
+    del x, W, Bt
+    nd = workloads.config_n("cuda", parts=("rmsnorm", "softmax", "sum"))
+    X, w = cpu(nd["rmsnorm"])
+    rn, O = RmsNormOp(64, 4096, dtype=torch.bfloat16, weighted=True), torch.empty(64, 4096, dtype=torch.bfloat16)
+    rec("rmsnorm_bf16_64x4096", lambda: rn(X, w, O), 1_056_768)
+    Xs = nd["softmax"].cpu()
+    Os = torch.empty_like(Xs)
+    sm = SoftmaxOp(4096, 32768)
+    rec("softmax_f32_4096x32768", lambda: sm(Xs, Os), 1_073_741_824)
+    del Xs, Os
+    A, Ao = nd["sum"].cpu(), torch.empty(1)
+    rd = ReduceOp(1 << 28)
+    rec("sum_f32_2^28", lambda: rd(A, Ao), 1_073_741_828)
+    del A, nd
+    torch.cuda.empty_cache()
+    Q, K, V = workloads.config_a("cuda")
+    Q, K, V = Q[:4].cpu(), K[:4].cpu(), V[:4].cpu()
+    at = AttnDecodeOp(4, 32, 8192, 128, num_kv_heads=8)
+    rec("gqa_decode_b32_h32_kv8_s8192", lambda: at(Q, K, V), 1_074_266_112, scale=8,
+        sample="4 of the 32 sequences timed, x8")
+    del Q, K, V
+    torch.cuda.empty_cache()
+    pos, *f1 = workloads.config_f1(1, "cuda")
+    f1 = cpu(f1)
+    qk = FusedQkNormRopeOp(1, 32, 128, 32768, pos, num_kv_heads=8)
+    rec("qk_norm_rope_b1", lambda: qk(*f1), 27_648)
+    del f1
+    f2 = cpu(workloads.config_f2(1, "cuda"))
+    ff = FusedOProjFfnOp(1, 4096, 12288, 32, 128)
+    rec("o_proj_ffn_b1", lambda: ff(*f2), 335_544_320 + 24_576 + 8_192)
+    del f2
+    torch.cuda.empty_cache()
+    B = layer_data[0].shape[0]
+    ld = cpu(layer_data)
+    lop = Qwen3DenseDecodeOp(B, SEQ_MAX, kv_lens=lens, norm_weights=True, rope_theta=1e6, **QWEN3_8B)
+    out = {}
+    rec("qwen3_layer", lambda: out.__setitem__("y", lop(*ld)), layer_bytes(B, lens))
+    return {"ops": ops, "layer_out": out["y"], "threads": threads, "cpu": cpu_model()}
 
 
-def op_table(torch, _hip, flush, peak_gbps: float) -> dict:
+def op_table(torch, _hip, flush) -> dict:
     """Per-op latency / GB/s for the other BASELINE configs.
 
     Each op is launched back to back inside one graph, rotating through enough
@@ -245,9 +301,9 @@ def op_table(torch, _hip, flush, peak_gbps: float) -> dict:
         ts = time_graph(chain, 10, 2, flush)
         us = statistics.median(ts) * 1e3 / n_launch
         gbps = nbytes / (us * 1e-6) / 1e9
-        out[name] = {"us": round(us, 2), "GBps": round(gbps, 1), "sol": round(gbps / peak_gbps, 4),
-                     "bytes": nbytes, "launches_per_graph": n_launch, **extra}
-        log(f"{name}: {us:.2f} us, {gbps:.0f} GB/s, sol {gbps / peak_gbps:.3f}")
+        out[name] = {"us": round(us, 2), "GBps": round(gbps, 1), "bytes": nbytes, "launches_per_graph": n_launch,
+                     **extra}
+        log(f"{name}: {us:.2f} us, {gbps:.0f} GB/s")
 
     def randn(*shape, dtype=torch.bfloat16, std=1.0, mean=0.0):
         return (torch.randn(*shape, generator=gcu, device="cuda") * std + mean).to(dtype)
@@ -324,8 +380,25 @@ def profile_only(torch, _hip, flush, args) -> int:
              calibration kernel for FETCH_SIZE / WRITE_SIZE.
     layer:   one full B=1 layer step.
     prefill: one Qwen3-8B layer prefill over a fresh 4096-token prompt.
+    gemv:    the config-G GEMV (4096 x 4096 bf16, 33,570,816 algorithmic bytes).
+    attn_a:  the config-A GQA decode (B=32, 32/8 heads, S=8192; 1,074,266,112 bytes).
     """
-    if args.profile_kernel == "prefill":
+    if args.profile_kernel in ("gemv", "attn_a"):
+        from ezops import AttnDecodeOp, GemvOp, workloads
+
+        if args.profile_kernel == "gemv":
+            x, W = workloads.config_g("cuda")
+            y = torch.empty(4096, dtype=torch.bfloat16, device="cuda")
+            g = GemvOp(4096, 4096, backend="hip")
+            fn = lambda: g(x, W, y)  # noqa: E731
+        else:
+            Q, K, V = workloads.config_a("cuda")
+            at = AttnDecodeOp(32, 32, 8192, 128, backend="hip", num_kv_heads=8)
+            fn = lambda: at(Q, K, V)  # noqa: E731
+        for _ in range(10):
+            flush()
+            fn()
+    elif args.profile_kernel == "prefill":
         from ezops import Qwen3PrefillOp
 
         op = Qwen3PrefillOp(1, 4096, q_lens=[4096], backend="hip", norm_weights=True, rope_theta=1e6, **QWEN3_8B)
@@ -370,7 +443,7 @@ def main() -> int:
     ap.add_argument("--no-step", action="store_true", help="skip the 36-layer decode-step timing")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill timings")
     ap.add_argument("--batch", type=int, default=1, help="layer batch (headline is 1)")
-    ap.add_argument("--profile-kernel", choices=["gate_up", "copy", "layer", "prefill"],
+    ap.add_argument("--profile-kernel", choices=["gate_up", "copy", "layer", "prefill", "gemv", "attn_a"],
                     help="only launch this kernel 10x between read flushes (for rocprofv3 counter runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -378,7 +451,6 @@ def main() -> int:
               "(the decode ops run on one MI355X; multi-GPU sharding is designed, not built).", file=sys.stderr)
         return 2
 
-    import numpy as np
     import torch
 
     from ezops import _hip
@@ -393,9 +465,12 @@ def main() -> int:
     if args.profile_kernel:
         return profile_only(torch, _hip, flush_cache, args)
 
-    log("measuring HBM peak (STREAM triad over 3 x 1 GiB)")
+    log("measuring HBM peak (STREAM probes over 2 GiB arrays)")
     peaks = hbm_peak(torch, _hip)
-    peak = peaks["triad"]
+    # The measured peak is the best sustained probe: the non-temporal read.
+    # (A triad mixes reads with writes and its read/write turnarounds cost
+    # ~15% on HBM3E, so kernels that only read beat it.)
+    peak = max(peaks.values())
     log(f"HBM triad {peaks['triad']:.0f} GB/s, read {peaks['read']:.0f} GB/s, streaming read "
         f"{peaks['read_nt']:.0f} GB/s, copy {peaks['copy']:.0f} GB/s")
 
@@ -487,7 +562,7 @@ def main() -> int:
     result = {
         "metric": METRIC,
         "value": round(gbps / peak, 4),
-        "unit": "fraction of measured HBM peak (STREAM triad)",
+        "unit": "fraction of measured HBM peak (best sustained probe: non-temporal read)",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -502,7 +577,7 @@ def main() -> int:
         "achieved_GBps": round(gbps, 1),
         "hbm_peak_measured_GBps": round(peak, 1),
         "hbm_probe_GBps": {k: round(v, 1) for k, v in peaks.items()},
-        "frac_of_read_peak": round(gbps / peaks["read_nt"], 4),
+        "frac_of_triad": round(gbps / peaks["triad"], 4),
         "sol_vs_spec_8TBps": round(gbps / SPEC_HBM_GBPS, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -516,7 +591,6 @@ def main() -> int:
         "roofline": {"kernel": "gemv_rows_kernel (RMSNorm + gate/up + SwiGLU stage)", "bound": "hbm",
                      "achieved": round(gu_gbps, 1), "peak": SPEC_HBM_GBPS, "unit": "GB/s",
                      "frac": round(gu_gbps / SPEC_HBM_GBPS, 4), "frac_of_measured_peak": round(gu_gbps / peak, 4),
-                     "frac_of_read_peak": round(gu_gbps / peaks["read_nt"], 4),
                      "us": round(gu_ms * 1e3, 2), "algorithmic_bytes": gu_bytes, "traffic": traffic,
                      "traffic_source": "profiles/gate_up_b1_traffic.json (FETCH_SIZE x2.0 + WRITE_SIZE x1.0)",
                      "timing": f"HIP events over {n_launch} back-to-back launches per graph replay, "
@@ -534,19 +608,31 @@ def main() -> int:
         log(f"prefill layer {result['prefill']['layer_T4096']['ms']:.3f} ms, "
             f"attention 16K {result['prefill']['attention_T16384']['TFLOPs']:.0f} TFLOP/s")
     if not args.no_cpu:
-        log("CPU baseline: numpy oracle of the same layer step")
-        cb = cpu_baseline(torch, op, data, lens)
-        ref = cb["out"]
-        err = float(np.linalg.norm(out.float().cpu().numpy() - ref) / max(np.linalg.norm(ref), 1.0))
-        result["parity_rel_frobenius"] = err
-        result["cpu_baseline"] = {"value": round(cb["sec"] * 1e6, 1), "unit": "us per layer",
-                                  "GBps": round(nbytes / cb["sec"] / 1e9, 2), "cores": cb["threads"],
-                                  "cpu": platform.processor() or platform.machine(), "kind": "port",
-                                  "sample": f"full layer step, batch {B}, median of {cb['reps']} runs "
-                                            "(oracle/ops.py qwen3_layer, numpy fp32 BLAS)"}
-        log(f"CPU baseline {cb['sec'] * 1e3:.1f} ms/layer; parity rel err {err:.2e}")
+        log("CPU baseline: the reference's torch path (backend 'ref') on the host cores")
+        cb = cpu_ref_baseline(torch, data, lens)
+        ref = cb["layer_out"].float()
+        err = float((out.float().cpu() - ref).norm() / max(ref.norm().item(), 1.0))
+        result["parity_rel_frobenius_vs_cpu_ref"] = err
+        lay = cb["ops"].pop("qwen3_layer")
+        result["cpu_baseline"] = {"value": lay["us"], "unit": "us per layer", "GBps": lay["GBps"],
+                                  "cores": cb["threads"], "cpu": cb["cpu"], "kind": "port",
+                                  "sample": f"the whole config-L layer step at batch {B} through the package's "
+                                            "backend='ref' torch path (the reference's _ref_forward formulas, "
+                                            f"bf16 CPU tensors), median of {lay['reps']} runs after 2 warm-ups",
+                                  "ops": cb["ops"]}
+        log(f"CPU baseline {lay['us'] / 1e3:.1f} ms/layer; GPU vs CPU ref rel err {err:.2e}")
     if not args.no_ops:
-        result["ops"] = op_table(torch, _hip, flush_cache, peak)
+        result["ops"] = op_table(torch, _hip, flush_cache)
+        best_op = max([v["GBps"] for v in result["ops"].values()] + [gu_gbps])
+        if best_op > peak:  # a kernel out-read every probe: it is the best sustained rate seen
+            peak = best_op
+            result["hbm_peak_source"] = "fastest kernel of this run (above every probe)"
+        for v in result["ops"].values():
+            v["sol"] = round(v["GBps"] / peak, 4)
+            v["sol_vs_spec_8TBps"] = round(v["GBps"] / SPEC_HBM_GBPS, 4)
+    result["value"] = round(gbps / peak, 4)
+    result["hbm_peak_measured_GBps"] = round(peak, 1)
+    result["roofline"]["frac_of_measured_peak"] = round(gu_gbps / peak, 4)
     print(json.dumps(result), flush=True)
     return 0
 

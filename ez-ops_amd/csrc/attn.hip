@@ -41,9 +41,6 @@
 #ifndef EZ_ATTN_TARGET4
 #define EZ_ATTN_TARGET4 8  // 4-wave blocks planned per CU
 #endif
-#ifndef EZ_ATTN_TRACE
-#define EZ_ATTN_TRACE 0  // timing experiments only: per-wave phase timestamps
-#endif
 
 namespace ez {
 
@@ -53,18 +50,6 @@ namespace {
 constexpr int kTile = 32;       // positions per wave iteration
 constexpr int kMaxSplits = 32;  // split partials the combine holds per lane
 constexpr float kLog2e = 1.4426950408889634f;
-
-#if EZ_ATTN_TRACE
-__device__ long long ez_attn_trace[65536 * 8];  // [block][wave][8] s_memrealtime stamps
-#define EZ_TRACE(k)                                                                                      \
-  do {                                                                                                   \
-    if (lane == 0) ez_attn_trace[(blockIdx.x * W + wave) * 8 + (k)] = __builtin_amdgcn_s_memrealtime(); \
-  } while (0)
-#else
-#define EZ_TRACE(k) \
-  do {              \
-  } while (0)
-#endif
 
 // Where the cache rows of one (sequence, kv head) unit live.  Contiguous:
 // one S x D slab.  Paged: page j of the sequence is pool page bt[j], each
@@ -257,7 +242,6 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar tile loop
-  EZ_TRACE(0);
   const int li = lane & 15, lg = lane >> 4;
   int split, kvh, b, nsb = nsplit;  // nsb: splits of this block's sequence
   if (a.split_chunk > 0) {
@@ -328,7 +312,6 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
 
   int64_t L = a.kv_lens ? int64_t(Lraw) : a.S;
   L = L < 0 ? 0 : (L > a.Lh ? a.Lh : L);
-  EZ_TRACE(1);
   // Cache rows read here: [0, Lc) (the layer's decoded token is the virtual row).
   const int64_t Lc = LAYER ? (L > 0 ? L - 1 : 0) : L;
   const int64_t cl = Lc > 0 ? Lc - 1 : 0;  // clamp row of later tiles
@@ -396,7 +379,6 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
 #pragma unroll
   for (int db = 0; db < NDB; ++db) o[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  EZ_TRACE(2);
   for (int it = 0; t0 < Lc; t0 += stride, ++it) {
     const int64_t tn = t0 + stride;
     // ---- S^T = K Q^T: acc[u][r] = S[head li][pos t0 + 16u + 4lg + r]
@@ -407,10 +389,6 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
 #pragma unroll
       for (int s = 0; s < NS; ++s)
         acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf[u][s]), qf[s], acc[u], 0, 0, 0);
-    }
-    if (EZ_ATTN_TRACE && it < 2) {
-      if (acc[0][0] == 1.2345e-30f) a.Out[0] = 1;  // the stamp follows the MFMA results
-      EZ_TRACE(3 + it);
     }
     const int64_t tsn = tile_start(tn, cl);
     const int32_t id_n = id_next;
@@ -506,7 +484,6 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
     }
   }
 
-  EZ_TRACE(5);
   if (li < G) {
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
@@ -546,7 +523,6 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
       }
     }
   }
-  EZ_TRACE(6);
 }
 
 // Merge of one query head (b, h) with one thread per head dim: every thread
@@ -700,17 +676,6 @@ int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
 }
 
 }  // namespace ez
-
-#if EZ_ATTN_TRACE
-extern "C" int ezops_attn_trace_read(void* host, size_t bytes) {
-  if (!host) {
-    void* p = nullptr;
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(ez::ez_attn_trace)) != hipSuccess) return -1;
-    return int(hipMemset(p, 0, bytes));
-  }
-  return int(hipMemcpyFromSymbol(host, HIP_SYMBOL(ez::ez_attn_trace), bytes, 0, hipMemcpyDeviceToHost));
-}
-#endif
 
 extern "C" size_t ezops_attn_decode_workspace_size(int64_t B, int64_t H, int64_t Hkv, int64_t S, int64_t D) {
   return ez::attn_workspace_size(B, H, Hkv, S, D);

@@ -407,8 +407,10 @@ extern "C" int ezops_softmax_f32(const float* X, float* Out, int64_t rows, int64
 }
 
 extern "C" size_t ezops_reduce_sum_workspace_size(int64_t n) {
-  // partial sums + one arrival counter, 256-byte aligned
-  return size_t(((sum_blocks(n) * 4 + 255) / 256) * 256 + 256);
+  // one arrival counter in bytes [0, 256), then the partial sums.  The
+  // counter's offset does not depend on n, so one workspace serves calls of
+  // any length (each call leaves the counter at zero again).
+  return size_t(256 + ((sum_blocks(n) * 4 + 255) / 256) * 256);
 }
 
 extern "C" int ezops_reduce_sum_f32(const float* A, float* Out, int64_t n, void* ws, size_t ws_bytes,
@@ -417,8 +419,8 @@ extern "C" int ezops_reduce_sum_f32(const float* A, float* Out, int64_t n, void*
   EZ_REQUIRE(n >= 1, "reduce_sum_f32: n must be >= 1");
   EZ_REQUIRE(ws_bytes >= ezops_reduce_sum_workspace_size(n), "reduce_sum_f32: workspace too small");
   const int64_t G = sum_blocks(n);
-  float* partial = static_cast<float*>(ws);
-  int* counter = reinterpret_cast<int*>(static_cast<char*>(ws) + ((G * 4 + 255) / 256) * 256);
+  int* counter = static_cast<int*>(ws);
+  float* partial = reinterpret_cast<float*>(static_cast<char*>(ws) + 256);
   hipLaunchKernelGGL(sum_kernel, dim3(unsigned(G)), dim3(kSumBlock), 0, s, A, n, aligned16(A), partial,
                      counter, Out);
   return launch_status("reduce_sum_f32");
@@ -426,12 +428,27 @@ extern "C" int ezops_reduce_sum_f32(const float* A, float* Out, int64_t n, void*
 
 // MFMA peak probe: every wave keeps 8 independent 16x16x32 accumulator chains
 // busy for `iters` rounds (operands built from the lane id, so nothing folds).
-// One launch performs blocks * 4 waves * iters * 8 * 16384 flops.
+// One launch performs blocks * 4 waves * iters * 8 * 16384 flops (kinds 0-2)
+// or blocks * 4 * iters * 8 * 2048 (kind 3, fp32 16x16x4).
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 template <int F16>
 __global__ __launch_bounds__(256) void probe_mfma_kernel(float* __restrict__ out, int64_t iters) {
   const float lf = float(threadIdx.x & 63) * (1.0f / 64.0f);
+  if constexpr (F16 == 3) {  // fp32 v_mfma_f32_16x16x4_f32: 8 chains, 2048 flops per instruction
+    f32x4_t acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const float a = lf, b = 1.0f - lf;
+    for (int64_t i = 0; i < iters; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[j], 0, 0, 0);
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sum += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
+    if (sum == 1234.5f) out[0] = sum;
+    return;
+  }
   if constexpr (F16 == 2) {  // bf16 32x32x16: 4 chains of 16-float accumulators, same flops per round
     f32x16_t acc[4];
 #pragma unroll
@@ -477,11 +494,12 @@ __global__ __launch_bounds__(256) void probe_mfma_kernel(float* __restrict__ out
 }
 
 extern "C" int ezops_mfma_probe(int kind, float* out, int64_t blocks, int64_t iters, hipStream_t s) {
-  EZ_REQUIRE(kind >= 0 && kind <= 2, "mfma_probe: kind must be 0 (bf16), 1 (fp16) or 2 (bf16 32x32x16)");
+  EZ_REQUIRE(kind >= 0 && kind <= 3, "mfma_probe: kind must be 0 (bf16), 1 (fp16), 2 (bf16 32x32x16) or 3 (fp32)");
   EZ_REQUIRE(out && blocks >= 1 && blocks < (int64_t(1) << 31) && iters >= 1, "mfma_probe: bad arguments");
   if (kind == 0) hipLaunchKernelGGL(probe_mfma_kernel<0>, dim3(unsigned(blocks)), dim3(256), 0, s, out, iters);
   else if (kind == 1) hipLaunchKernelGGL(probe_mfma_kernel<1>, dim3(unsigned(blocks)), dim3(256), 0, s, out, iters);
-  else hipLaunchKernelGGL(probe_mfma_kernel<2>, dim3(unsigned(blocks)), dim3(256), 0, s, out, iters);
+  else if (kind == 2) hipLaunchKernelGGL(probe_mfma_kernel<2>, dim3(unsigned(blocks)), dim3(256), 0, s, out, iters);
+  else hipLaunchKernelGGL(probe_mfma_kernel<3>, dim3(unsigned(blocks)), dim3(256), 0, s, out, iters);
   return launch_status("mfma_probe");
 }
 

@@ -36,8 +36,8 @@ SPECS = {
     },
 }
 
-_MFMA_KINDS = {"bf16": 0, "fp16": 1, "bf16_32x32": 2}
-_MFMA_FLOPS_PER_INSTR = 2 * 16 * 16 * 32
+_MFMA_KINDS = {"bf16": 0, "fp16": 1, "bf16_32x32": 2, "fp32": 3}
+_MFMA_FLOPS_PER_INSTR = {0: 2 * 16 * 16 * 32, 1: 2 * 16 * 16 * 32, 2: 2 * 16 * 16 * 32, 3: 2 * 16 * 16 * 4}
 
 
 def detect_profile(name: str = "", arch: str = "") -> str | None:
@@ -82,7 +82,8 @@ def measure_hbm(n_bytes_per_array: int = 2 << 30, reps: int = 10) -> dict:
 
 
 def measure_mfma(dtype: str = "bf16", iters: int = 4096, reps: int = 10) -> float:
-    """Dense MFMA throughput (TFLOP/s) of independent v_mfma_f32_16x16x32 chains on every SIMD."""
+    """Dense MFMA throughput (TFLOP/s) of independent MFMA chains on every SIMD
+    (16x16x32 for bf16 / fp16, 32x32x16 for "bf16_32x32", 16x16x4 for fp32)."""
     import torch
 
     from . import _hip
@@ -90,7 +91,7 @@ def measure_mfma(dtype: str = "bf16", iters: int = 4096, reps: int = 10) -> floa
     blocks = torch.cuda.get_device_properties(0).multi_processor_count * 8
     sink = torch.zeros(4, device="cuda")
     s = _hip.stream()
-    flops = blocks * 4 * iters * 8 * _MFMA_FLOPS_PER_INSTR
+    flops = blocks * 4 * iters * 8 * _MFMA_FLOPS_PER_INSTR[_MFMA_KINDS[dtype]]
     best = math.inf
     for _ in range(reps + 2):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -109,11 +110,24 @@ def _fmt(coeff: float, unit_exp: int) -> str:
 
 
 def generate_yaml(profile: str, gpu_name: str, hbm: dict, mfma_tflops: dict) -> str:
-    """Profile YAML in the reference's layout (assets/rtx_5060_ti.yaml)."""
+    """Profile YAML in the reference's layout (assets/rtx_5060_ti.yaml).
+
+    ``hbm.calibration`` is the best sustained rate measured (the streaming
+    read when it is given, else the triad): the reference's benches divide by
+    ``theoretical * calibration`` (benchmarks/bench_gemv.py:62-86), and a
+    denominator that the chip's own read-only kernels beat is not a peak.
+    The triad is kept as ``triad_calibration``.
+
+    ``tensor_core.tf32``: gfx950 has no TF32 matrix type (xf32 was dropped
+    after CDNA3); fp32 GEMMs run on the fp32 MFMA at the fp32 rate, so the
+    tf32 entry -- the FP32 compute ceiling the reference's ``_compute_sol``
+    reads -- carries the fp32 matrix peak and its calibration."""
     spec = SPECS[profile]
+    best = max(hbm.values())
+    src = "streaming read (non-temporal)" if "read" in hbm and hbm["read"] >= best else "STREAM Triad"
     lines = [
         f"# GPU Profile: {gpu_name}",
-        "# Calibration: ezops_hbm_probe (STREAM triad, 3 x 2 GiB) and ezops_mfma_probe",
+        "# Calibration: ezops_hbm_probe (STREAM probes over 2 GiB arrays) and ezops_mfma_probe",
         "# Written by: cd ez-ops_amd && python -m ezops.hardware",
         "#",
         "# Only store theoretical + calibration here.",
@@ -129,16 +143,22 @@ def generate_yaml(profile: str, gpu_name: str, hbm: dict, mfma_tflops: dict) -> 
         "",
         "hbm:",
         f"  theoretical: {_fmt(spec['hbm_bw_gb'], 9)}        # bytes/s, spec sheet",
-        f"  calibration: {hbm['triad'] / spec['hbm_bw_gb']:.3f}         # STREAM Triad",
+        f"  calibration: {best / spec['hbm_bw_gb']:.3f}         # best sustained: {src}",
     ]
+    if "triad" in hbm:
+        lines.append(f"  triad_calibration: {hbm['triad'] / spec['hbm_bw_gb']:.3f}   # STREAM Triad")
     if "read" in hbm:
         lines.append(f"  read_calibration: {hbm['read'] / spec['hbm_bw_gb']:.3f}    # streaming read (non-temporal)")
     lines += ["", "tensor_core:"]
-    for dtype, theo in spec["tensor_core_tflops"].items():
+    entries = dict(spec["tensor_core_tflops"])
+    entries["tf32"] = entries["fp32"]
+    for dtype, theo in entries.items():
+        meas = mfma_tflops.get("fp32" if dtype == "tf32" else dtype)
+        note = "  (no TF32 type on gfx950: the fp32 MFMA peak)" if dtype == "tf32" else ""
         lines.append(f"  {dtype}:")
-        lines.append(f"    theoretical: {_fmt(theo, 12)}     # FLOPS, spec sheet (dense)")
-        if dtype in mfma_tflops:
-            lines.append(f"    calibration: {mfma_tflops[dtype] / theo:.2f}")
+        lines.append(f"    theoretical: {_fmt(theo, 12)}     # FLOPS, spec sheet (dense){note}")
+        if meas is not None:
+            lines.append(f"    calibration: {meas / theo:.2f}")
         lines.append("")
     return "\n".join(lines)
 
@@ -153,8 +173,9 @@ def load_profile(name_or_path: str | Path = "mi355x") -> dict:
     prof = yaml.safe_load(path.read_text())
     hbm = prof["hbm"]
     hbm["effective"] = float(hbm["theoretical"]) * float(hbm.get("calibration", 1.0))
-    if "read_calibration" in hbm:
-        hbm["read_effective"] = float(hbm["theoretical"]) * float(hbm["read_calibration"])
+    for key in ("read", "triad"):
+        if f"{key}_calibration" in hbm:
+            hbm[f"{key}_effective"] = float(hbm["theoretical"]) * float(hbm[f"{key}_calibration"])
     for entry in prof.get("tensor_core", {}).values():
         entry["effective"] = float(entry["theoretical"]) * float(entry.get("calibration", 1.0))
     return prof
@@ -163,7 +184,7 @@ def load_profile(name_or_path: str | Path = "mi355x") -> dict:
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description="Generate the MI355X roofline profile YAML")
     ap.add_argument("--output-dir", default=str(ASSETS))
-    ap.add_argument("--dtypes", default="bf16")
+    ap.add_argument("--dtypes", default="bf16,fp32")
     args = ap.parse_args(argv)
 
     import torch
@@ -174,11 +195,11 @@ def main(argv=None) -> int:
         print(f"unknown device {props.name!r}: only the MI355X profile is defined")
         return 2
     hbm = measure_hbm()
-    print(f"HBM triad {hbm['triad']:.0f} GB/s, streaming read {hbm['read']:.0f} GB/s")
+    print(f"HBM triad {hbm['triad']:.0f} GB/s, streaming read {hbm['read']:.0f} GB/s (calibration: the best)")
     mfma = {}
     for dtype in [d.strip() for d in args.dtypes.split(",") if d.strip()]:
         mfma[dtype] = measure_mfma(dtype)
-        print(f"MFMA {dtype} 16x16x32: {mfma[dtype]:.0f} TFLOP/s")
+        print(f"MFMA {dtype}: {mfma[dtype]:.0f} TFLOP/s")
         if dtype == "bf16":  # the larger tile shape can issue denser; keep the faster
             big = measure_mfma("bf16_32x32")
             print(f"MFMA bf16 32x32x16: {big:.0f} TFLOP/s")

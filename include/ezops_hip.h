@@ -99,7 +99,7 @@ int ezops_reduce_sum_f32(const float* A, float* Out, int64_t n, void* workspace,
 
 /* Split-KV GQA decode attention, one query token per sequence.
  * Q [B, H, D] (== [B, H, 1, D]), K/V [B, Hkv, S, D], Out [B, H, D]; bf16.
- * H % Hkv == 0, H / Hkv <= 16, D in {64, 128}.  kv_lens [B] int32 (NULL = S
+ * H % Hkv == 0, H / Hkv in {1, 2, 4, 8}, D in {64, 128}.  kv_lens [B] int32 (NULL = S
  * for every sequence) limits sequence b to slots [0, kv_lens[b]).
  * max_kv_len: the caller's bound on the kv_lens entries (0 = S), used to plan
  * the split-KV grid and to request the first K/V tiles before the lengths
@@ -184,6 +184,9 @@ int ezops_o_proj_ffn_bf16(const void* attn, const void* residual, const void* Wo
                           void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* One Qwen3 dense decoder-layer decode step (see ezops/ops/qwen3_dense_decode.py).
+ * The attention stage has the limits of ezops_attn_decode_bf16: H / Hkv in
+ * {1, 2, 4, 8} and D in {64, 128} (EZOPS_EINVAL otherwise); the same holds
+ * for the paged layer and the multi-layer step below.
  * Replaces: Qwen3DenseDecodeOp backends (ezops/kernels/qwen3_dense_decode/
  * qwen3_dense_decode_triton.py:273-384, qwen3_dense_decode_persistent_tl.py:566-609). */
 typedef struct ezops_qwen3_layer {
@@ -310,8 +313,9 @@ int ezops_hbm_probe(int kind, float* a, const float* b, const float* c, int64_t 
 /* MFMA peak probe for the hardware profile (replaces the torch-matmul sweep of
  * benchmarks/hardware/compute/matmul_peak.py, used by
  * scripts/roofline_profile.py:171-199): kind 0 = bf16, 1 = fp16
- * v_mfma_f32_16x16x32 chains, 2 = bf16 v_mfma_f32_32x32x16 chains; every kind
- * performs blocks * 4 * iters * 8 * 16384 flops per launch. */
+ * v_mfma_f32_16x16x32 chains, 2 = bf16 v_mfma_f32_32x32x16 chains (each
+ * blocks * 4 * iters * 8 * 16384 flops per launch), 3 = fp32
+ * v_mfma_f32_16x16x4_f32 chains (blocks * 4 * iters * 8 * 2048 flops). */
 int ezops_mfma_probe(int kind, float* out, int64_t blocks, int64_t iters, hipStream_t stream);
 
 #ifdef __cplusplus

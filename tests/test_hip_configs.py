@@ -1,0 +1,134 @@
+"""Every benchmark configuration at its own full size, HIP vs the numpy oracle (GPU).
+
+Inputs come from ezops.workloads (the configuration's seed and
+distributions, drawn on the GPU).  These are the launch plans the benchmark
+times: the B=32 non-ragged attention grid, the 32768-wide softmax rows, the
+2^28 sum's full grid, QK-norm+RoPE at Qwen3-8B heads over a 32768-row cache
+and the batch-16 Qwen3-8B layer over a 16384-row cache.
+
+Bars: bf16 allclose(atol 2e-2, rtol 1e-2) against the fp32-accumulated
+oracle; softmax atol 1e-6 / rtol 1e-5 (SoftmaxOp.check); sum atol 1e-7 * n
+(ReduceOp.check) and 1e-5 relative to the fp64 sum; fused ops relative
+Frobenius < 1e-2 (the ops' own check).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from ezops import (AttnDecodeOp, FusedOProjFfnOp, FusedQkNormRopeOp, GemvOp, ReduceOp, RmsNormOp,
+                   SoftmaxOp, workloads)
+
+pytestmark = pytest.mark.gpu
+BF_TOL = dict(rtol=1e-2, atol=2e-2)
+DEV = "cuda"
+
+
+def n(x):
+    return x.detach().float().cpu().numpy()
+
+
+def test_config_g_gemv():
+    x, W = workloads.config_g(DEV)
+    op = GemvOp(4096, 4096, backend="hip")
+    y = torch.empty(4096, dtype=torch.bfloat16, device=DEV)
+    op(x, W, y)
+    np.testing.assert_allclose(n(y), oracle.gemv(n(x), n(W)), **BF_TOL)
+
+
+def test_config_n_rmsnorm():
+    X, w = workloads.config_n(DEV, parts=("rmsnorm",))["rmsnorm"]
+    op = RmsNormOp(64, 4096, backend="hip", dtype=torch.bfloat16, weighted=True)
+    out = torch.empty_like(X)
+    op(X, w, out)
+    np.testing.assert_allclose(n(out), oracle.rmsnorm_bf16(n(X), n(w)), **BF_TOL)
+
+
+def test_config_n_softmax():
+    X = workloads.config_n(DEV, parts=("softmax",))["softmax"]
+    op = SoftmaxOp(4096, 32768, backend="hip")
+    out = torch.empty_like(X)
+    op(X, out)
+    Xh = n(X)
+    del X
+    for r0 in range(0, 4096, 512):  # the fp64 oracle in 512-row slices (1 GiB each)
+        ref = torch.from_numpy(oracle.softmax(Xh[r0:r0 + 512])).to(DEV)
+        assert op.check(out[r0:r0 + 512], ref), (r0, (out[r0:r0 + 512] - ref).abs().max().item())
+
+
+def test_config_n_sum():
+    A = workloads.config_n(DEV, parts=("sum",))["sum"]
+    op = ReduceOp(1 << 28, backend="hip")
+    out = torch.empty(1, device=DEV)
+    op(A, out)
+    ref64 = float(torch.sum(A.double()).item())
+    assert op.check(out, torch.tensor([ref64], dtype=torch.float32, device=DEV)), (out.item(), ref64)
+    assert abs(out.item() - ref64) <= 1e-5 * abs(ref64), (out.item(), ref64)
+    out2 = torch.empty(1, device=DEV)
+    op(A, out2)
+    assert torch.equal(out, out2)  # fixed summation order: bitwise repeatable
+
+
+def test_config_a_gqa_decode_b32():
+    """B=32 x 8 kv heads x S=8192 without kv_lens: the non-ragged 4-wave plan."""
+    Q, K, V = workloads.config_a(DEV)
+    op = AttnDecodeOp(32, 32, 8192, 128, backend="hip", num_kv_heads=8)
+    out = op(Q, K, V)
+    assert out.shape == (32, 32, 1, 128)
+    ref = oracle.attn_decode(n(Q)[:, :, 0], n(K), n(V))
+    np.testing.assert_allclose(n(out)[:, :, 0], ref, **BF_TOL)
+    assert torch.equal(out, op(Q, K, V))
+
+
+@pytest.mark.parametrize("B", [1, 16])
+def test_config_f1_qk_norm_rope(B):
+    """Qwen3-8B heads (32 / 8 x 128), positions ~ U[0, 32768) over a
+    32768-row cache: every sequence's slot holds the rotated k / raw v and
+    nothing else in the caches moves."""
+    pos, q, k, v, qw, kw, cos, sin, Kc, Vc = workloads.config_f1(B, DEV)
+    op = FusedQkNormRopeOp(B, 32, 128, 32768, pos, backend="hip", num_kv_heads=8)
+    K0, V0 = Kc.clone(), Vc.clone()
+    q_out, k_out = op(q, k, v, qw, kw, cos, sin, Kc, Vc)
+    slot = np.zeros((1, 8, 1, 128), np.float32)
+    for b, p in enumerate(pos):
+        # the oracle over a one-row table holding row p of cos / sin, one-row caches
+        rq, rk, rK, rV = oracle.qk_norm_rope(n(q[b:b + 1]), n(k[b:b + 1]), n(v[b:b + 1]), n(qw), n(kw),
+                                             n(cos[p:p + 1]), n(sin[p:p + 1]), slot, slot, 0)
+        np.testing.assert_allclose(n(q_out[b]), rq[0], **BF_TOL)
+        np.testing.assert_allclose(n(k_out[b]), rk[0], **BF_TOL)
+        assert torch.equal(Kc[b, :, p], k_out[b])
+        assert torch.equal(Vc[b, :, p], v[b])
+    # rows other than the written slot are untouched
+    for b, p in enumerate(pos):
+        Kc[b, :, p], Vc[b, :, p] = K0[b, :, p], V0[b, :, p]
+    assert torch.equal(Kc, K0) and torch.equal(Vc, V0)
+
+
+@pytest.mark.parametrize("B", [1, 16])
+def test_config_f2_o_proj_ffn(B):
+    args = workloads.config_f2(B, DEV)
+    op = FusedOProjFfnOp(B, 4096, 12288, 32, 128, backend="hip")
+    out = op(*args)
+    ref = torch.from_numpy(oracle.o_proj_ffn(*[n(x) for x in args])).to(DEV)
+    assert op.check(out, ref), (out.float() - ref).norm().item() / ref.norm().item()
+
+
+@pytest.mark.parametrize("B", [1, 16])
+def test_config_l_qwen3_layer(B):
+    """The Qwen3-8B layer with kv_lens ~ U[1024, 16384] over a 16384-row cache."""
+    op, data, lens = workloads.config_l(B, DEV)
+    K0, V0 = data[1].clone(), data[2].clone()
+    out = op(*data)
+    npy = [n(x) for x in data]
+    ref, rK, rV = oracle.qwen3_layer(npy[0], n(K0), n(V0), *npy[3:7], 32, 8, 128, kv_lens=lens,
+                                     in_norm_w=npy[7], q_norm_w=npy[8], k_norm_w=npy[9], post_norm_w=npy[10],
+                                     cos=npy[11], sin=npy[12])
+    ref_t = torch.from_numpy(ref).to(DEV)
+    assert op.check(out, ref_t), (out.float() - ref_t).norm().item() / ref_t.norm().item()
+    Kc, Vc = data[1], data[2]
+    for b, L in enumerate(lens):
+        np.testing.assert_allclose(n(Kc[b, :, L - 1]), rK[b, :, L - 1], **BF_TOL)
+        np.testing.assert_allclose(n(Vc[b, :, L - 1]), rV[b, :, L - 1], **BF_TOL)
+        Kc[b, :, L - 1], Vc[b, :, L - 1] = K0[b, :, L - 1], V0[b, :, L - 1]
+    assert torch.equal(Kc, K0) and torch.equal(Vc, V0)

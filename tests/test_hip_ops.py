@@ -101,6 +101,24 @@ def test_reduce(size):
     assert check_determinism(op, (A,), Out) and check_input_readonly(op, (A,), Out)
 
 
+def test_reduce_shared_workspace_across_lengths():
+    """One workspace serves calls of different lengths through the C ABI: the
+    arrival counter sits at a fixed offset, so a short call after a long one
+    (different block counts) still finds it at zero."""
+    n_big, n_small = 1 << 24, 8192 * 10
+    ws_bytes = _hip.size("ezops_reduce_sum_workspace_size", n_big)
+    assert ws_bytes >= _hip.size("ezops_reduce_sum_workspace_size", n_small)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=DEV)
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    for size in (n_big, n_small, n_big, 1):
+        A = torch.rand(size, generator=gen, device=DEV) * 2 - 1
+        out = torch.full((1,), float("nan"), device=DEV)
+        _hip.call("ezops_reduce_sum_f32", A.data_ptr(), out.data_ptr(), size, ws.data_ptr(), ws_bytes,
+                  _hip.stream())
+        torch.cuda.synchronize()
+        assert abs(out.item() - oracle.reduce_sum(n(A))[0]) <= 1e-7 * size, (size, out.item())
+
+
 def test_reduce_unaligned_view():
     base = torch.rand(4097, device=DEV) * 2 - 1
     A = base[1:]  # 4-byte offset: scalar path
