@@ -32,6 +32,8 @@
 // (max, sum, O) through LDS; with more than one split the blocks write fp32
 // partials that attn_combine_kernel merges (the kernel boundary orders the
 // hand-off; an in-kernel arrival counter measured no faster on MI355X).
+#include <mutex>
+
 #include "common.h"
 #include "internal.h"
 #include "prof.h"
@@ -676,6 +678,58 @@ int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
 }
 
 }  // namespace ez
+
+// ---------------------------------------------------------------------------
+// Allocation-free entry: the split partials live in a fixed device array
+// instead of a caller workspace.  Each GPU holds its own copy of `scratch`
+// (at its own address) until the process ends.  `scratch` is a host-side
+// stand-in in host code: its device address is looked up once per device
+// with hipGetSymbolAddress and only that address reaches a kernel.  Every
+// slot the combine reads is written by the same call, so nothing needs
+// clearing between calls; calls that overlap in time on one GPU race on it.
+constexpr size_t kAttnScratchBytes = size_t(8) << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kAttnScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return ez::set_error(int(e), "attn_decode_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return ez::set_error(EZ_EINVAL, "attn_decode_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return ez::set_error(e != hipSuccess ? int(e) : EZ_EINVAL, "attn_decode_noalloc: hipGetSymbolAddress: %s",
+                           hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return EZ_OK;
+}
+}  // namespace
+
+extern "C" size_t ezops_attn_decode_noalloc_max_scratch(void) { return kAttnScratchBytes; }
+
+extern "C" int ezops_attn_decode_noalloc_bf16(const void* Q, const void* K, const void* V, void* Out, int64_t B,
+                                              int64_t H, int64_t Hkv, int64_t S, int64_t D, const int32_t* kv_lens,
+                                              int64_t max_kv_len, float scale, hipStream_t stream) {
+  EZ_REQUIRE(Q, "attn_decode_noalloc: null pointer");
+  const size_t need = ez::attn_workspace_size(B, H, Hkv, S, D);
+  EZ_REQUIRE(need <= kAttnScratchBytes,
+             "attn_decode_noalloc: split partials need %zu bytes, above the %zu-byte device scratch", need,
+             kAttnScratchBytes);
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != EZ_OK) return rc;
+  return ezops_attn_decode_bf16(Q, K, V, Out, B, H, Hkv, S, D, kv_lens, max_kv_len, scale, ws, kAttnScratchBytes,
+                                stream);
+}
 
 extern "C" size_t ezops_attn_decode_workspace_size(int64_t B, int64_t H, int64_t Hkv, int64_t S, int64_t D) {
   return ez::attn_workspace_size(B, H, Hkv, S, D);

@@ -50,6 +50,8 @@ SIGNATURES: dict[str, tuple] = {
     "ezops_reduce_sum_f32": (_i32, [_p, _p, _i64, _p, _sz, _p]),
     "ezops_attn_decode_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64]),
     "ezops_attn_decode_bf16": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _f32, _p, _sz, _p]),
+    "ezops_attn_decode_noalloc_max_scratch": (_sz, []),
+    "ezops_attn_decode_noalloc_bf16": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _f32, _p]),
     "ezops_prefill_attn_bf16": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64,
                                        _i64, _f32, _p]),
     "ezops_qwen3_prefill_workspace_size": (_sz, [C.POINTER(Qwen3LayerParams), _i64]),

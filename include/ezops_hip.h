@@ -115,6 +115,22 @@ int ezops_attn_decode_bf16(const void* Q, const void* K, const void* V, void* Ou
                            int64_t max_kv_len, float scale, void* workspace,
                            size_t workspace_bytes, hipStream_t stream);
 
+/* The same decode attention without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture that may not
+ * call hipMalloc, tight serving loops, harnesses that forbid allocation).
+ * No counterpart in the reference.  The split partials live in a fixed
+ * device array of ezops_attn_decode_noalloc_max_scratch() bytes (8 MiB),
+ * one per GPU, held until the process ends; shapes whose partials need more
+ * (ezops_attn_decode_workspace_size above that) return EZOPS_EINVAL.  Nothing
+ * is allocated, and every result equals ezops_attn_decode_bf16 bit for bit.
+ * Calls that overlap in time on one GPU share the array and race: order
+ * them on one stream.  The first call on a device looks up the array's
+ * address (not capturable: make it once eagerly before a graph capture). */
+size_t ezops_attn_decode_noalloc_max_scratch(void);
+int ezops_attn_decode_noalloc_bf16(const void* Q, const void* K, const void* V, void* Out, int64_t B,
+                                   int64_t H, int64_t Hkv, int64_t S, int64_t D, const int32_t* kv_lens,
+                                   int64_t max_kv_len, float scale, hipStream_t stream);
+
 /* The same decode attention over a paged KV cache (block tables).
  * K_pages / V_pages [num_pages, Hkv, page_size, D] bf16 page pools;
  * block_table [B, max_pages] int32: logical page j of sequence b (cache rows
