@@ -143,7 +143,7 @@ def decode_step(torch, data, lens, batch: int, steps: int, warmup: int, flush) -
 
 def prefill(torch, flush) -> dict:
     """Prefill (the step before decode): one Qwen3-8B layer over a fresh
-    4096-token prompt (hipBLASLt GEMMs + causal MFMA flash attention + cache
+    4096-token prompt (own MFMA GEMMs + causal MFMA flash attention + cache
     write), and the attention kernel alone at 4K and 16K tokens, against the
     dense bf16 MFMA peak.  HIP events around each call, median of 5."""
     from ezops import PrefillAttnOp, Qwen3PrefillOp

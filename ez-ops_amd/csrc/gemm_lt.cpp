@@ -1,8 +1,9 @@
-// Plain bf16 GEMMs of the prefill stage through hipBLASLt:
+// bf16 GEMMs of the prefill stage:
 //   Y[M, N] = X[M, K] W[N, K]^T (+ R[M, N]), fp32 accumulation, bf16 out.
-// These are library GEMMs with no fused prologue (prefill has M = tokens in
-// the thousands, where the decode path's weight-streaming kernels do not
-// apply); the residual add rides on the GEMM's beta * C term.
+// Shapes with K % 64 == 0 and 16-byte aligned operands (every transformer
+// projection) run the own MFMA kernel (gemm.hip); the others fall back to a
+// hipBLASLt library GEMM, set up here, whose residual add rides on the
+// GEMM's beta * C term (one rounding instead of the MFMA kernel's two).
 //
 // hipBLASLt is column-major: the row-major Y^T is D (N x M, ld ldy), computed
 // as op(A) B with A = W viewed as a K x N column-major matrix (op T) and
@@ -129,6 +130,7 @@ int gemm_bf16(const uint16_t* X, int64_t ldx, const uint16_t* W, uint16_t* Y, in
               int64_t M, int64_t N, int64_t K, void* ws, size_t ws_bytes, hipStream_t s) {
   EZ_REQUIRE(X && W && Y, "gemm: null pointer");
   EZ_REQUIRE(M >= 1 && N >= 1 && K >= 1 && ldx >= K && ldy >= N, "gemm: bad shape");
+  if (gemm_mfma_supported(X, ldx, W, Y, ldy, R, M, N, K)) return gemm_mfma(X, ldx, W, Y, ldy, R, M, N, K, s);
   int dev = 0;
   EZ_REQUIRE(hipGetDevice(&dev) == hipSuccess, "gemm: no current device");
   hipblasLtHandle_t h = nullptr;

@@ -31,7 +31,7 @@ static_assert(sizeof(WaveRecord) == 32, "record layout is part of the profiling 
 
 enum ProfKernel : uint16_t {
   kProfGemvRows = 1, kProfGemvValu, kProfLinearScalar, kProfLinearMfma, kProfAttnSplit, kProfAttnCombine,
-  kProfPrefillAttn, kProfSiluMul, kProfQkRope, kProfRmsnormF32, kProfRmsnormBf16, kProfSoftmax, kProfSum,
+  kProfPrefillAttn, kProfSiluMul, kProfQkRope, kProfRmsnormF32, kProfRmsnormBf16, kProfSoftmax, kProfSum, kProfGemm,
 };
 
 // Records are appended per CU (region = XCC, SE, SH, CU from the hardware

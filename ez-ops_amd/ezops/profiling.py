@@ -54,7 +54,7 @@ assert RECORD_DTYPE.itemsize == 32
 KERNEL_NAMES = {
     1: "gemv_rows", 2: "gemv_valu", 3: "linear_scalar", 4: "linear_mfma", 5: "attn_split", 6: "attn_combine",
     7: "prefill_attn", 8: "silu_mul", 9: "qk_norm_rope", 10: "rmsnorm_f32", 11: "rmsnorm_bf16", 12: "softmax",
-    13: "sum",
+    13: "sum", 14: "gemm",
 }
 TICKS_PER_US = 100.0  # s_memrealtime runs at 100 MHz
 MAX_RECORDS = 1 << 21  # host buffer of a WaveTrace (64 MiB)

@@ -274,12 +274,11 @@ int ezops_qwen3_decode_step_bf16(const ezops_qwen3_layer* layers, int64_t n_laye
  * norm + RoPE at that position) and attends rows [0, kv_lens[b] + i].
  * p->max_kv_len is unused.  block_table != NULL: paged caches as in
  * ezops_qwen3_dense_decode_paged_bf16.  max_q_len: host bound on the
- * per-sequence token counts.  D = 128, IS % 8 == 0.  GEMMs run through
- * hipBLASLt (a shape's first call sets up its algorithm on the host; run it
- * eagerly once before capturing a graph).  The algorithm is the fastest of
- * the heuristic's candidates timed on that first call, so two processes may
- * keep different ones and agree only to bf16 rounding; within a process the
- * results are deterministic.
+ * per-sequence token counts.  D = 128, IS % 8 == 0.  The projections run
+ * the library's MFMA GEMM (see ezops_gemm_bf16) when HS, IS and H*D are
+ * multiples of 64 (deterministic, allocation-free); other shapes use
+ * hipBLASLt, whose first call of a shape sets up and times its algorithm on
+ * the host (run such shapes eagerly once before capturing a graph).
  * No counterpart in the reference (decode only,
  * ezops/ops/qwen3_dense_decode.py:9-176): the step that fills the cache the
  * decode layer reads. */
@@ -289,9 +288,12 @@ int ezops_qwen3_prefill_bf16(const ezops_qwen3_layer* p, int64_t T, const int32_
                              int64_t page_size, void* workspace, size_t workspace_bytes,
                              hipStream_t stream);
 
-/* Library GEMM used by prefill (hipBLASLt): Y[M, N] = X[M, K] W[N, K]^T,
- * plus R[M, N] (same leading dimension as Y) when R != NULL; bf16 in/out,
- * fp32 accumulation.  workspace: ezops_gemm_workspace_size() bytes.
+/* GEMM used by prefill: Y[M, N] = X[M, K] W[N, K]^T, and with R != NULL
+ * (R [M, N], same leading dimension as Y; may be Y) Y = bf16(R + bf16(X W^T));
+ * bf16 in/out, fp32 accumulation.  K % 64 == 0 with ldx % 8 == 0 and 16-byte
+ * aligned X and W runs the library's own MFMA kernel (no workspace used);
+ * other shapes fall back to hipBLASLt (the residual then rounds once:
+ * bf16(R + X W^T)).  workspace: ezops_gemm_workspace_size() bytes.
  * No counterpart in the reference (its GEMMs are decode GEMVs). */
 size_t ezops_gemm_workspace_size(void);
 int ezops_gemm_bf16(const void* X, int64_t ldx, const void* W, void* Y, int64_t ldy, const void* R,
@@ -307,7 +309,8 @@ int ezops_gemm_bf16(const void* X, int64_t ldx, const void* W, void* Y, int64_t 
  *   uint32 xcc_id   XCC_ID register (XCD in bits 3:0)
  *   uint16 kernel   kernel id (1 gemv_rows, 2 gemv_valu, 3 linear_scalar, 4 linear_mfma,
  *                   5 attn_split, 6 attn_combine, 7 prefill_attn, 8 silu_mul,
- *                   9 qk_norm_rope, 10 rmsnorm_f32, 11 rmsnorm_bf16, 12 softmax, 13 sum)
+ *                   9 qk_norm_rope, 10 rmsnorm_f32, 11 rmsnorm_bf16, 12 softmax, 13 sum,
+ *                   14 gemm)
  *   uint16 wave     wave index in its block;  uint32 block  blockIdx.x
  * ezops_profile_reset clears the buffers; ezops_profile_read copies up to
  * `capacity` records to host memory and returns how many (both synchronise

@@ -49,13 +49,17 @@ def test_prefill_attn_paged_equals_contiguous(page_size):
     assert torch.equal(out, cop(Q, K, V))
 
 
-# ---- prefill layer and its library GEMM
+# ---- prefill layer and its GEMM
 from ezops import Qwen3DenseDecodeOp, Qwen3PrefillOp, _hip  # noqa: E402
 
 QWEN3_8B = dict(hidden_size=4096, intermediate_size=12288, num_heads=32, head_dim=128)
 
 
-@pytest.mark.parametrize("M,N,K,resid", [(512, 6144, 4096, False), (77, 4096, 12288, True), (1, 200, 64, True)])
+@pytest.mark.parametrize("M,N,K,resid", [
+    (512, 6144, 4096, False), (77, 4096, 12288, True), (1, 200, 64, True),  # the MFMA kernel
+    (300, 520, 128, False), (256, 256, 64, True), (4096, 768, 4096, "alias"),  # tile tails, one tile, R = Y
+    (33, 100, 100, False), (5, 64, 72, True),  # K % 64 != 0: the hipBLASLt fallback
+])
 def test_gemm_vs_oracle(M, N, K, resid):
     rng = np.random.default_rng(M + N)
     X = oracle.bf16(rng.standard_normal((M, K)).astype(np.float32))
@@ -63,12 +67,18 @@ def test_gemm_vs_oracle(M, N, K, resid):
     R = oracle.bf16(rng.standard_normal((M, N)).astype(np.float32))
     g = lambda a: torch.from_numpy(a).to(torch.bfloat16).cuda()  # noqa: E731
     Xg, Wg, Rg = g(X), g(W), g(R)
-    Y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    Y = Rg.clone() if resid == "alias" else torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    Rp = Y.data_ptr() if resid == "alias" else (Rg.data_ptr() if resid else None)
     ws = torch.empty(_hip.size("ezops_gemm_workspace_size"), dtype=torch.uint8, device="cuda")
-    _hip.call("ezops_gemm_bf16", Xg.data_ptr(), K, Wg.data_ptr(), Y.data_ptr(), N, Rg.data_ptr() if resid else None,
-              M, N, K, ws.data_ptr(), ws.numel(), _hip.stream())
+    _hip.call("ezops_gemm_bf16", Xg.data_ptr(), K, Wg.data_ptr(), Y.data_ptr(), N, Rp, M, N, K, ws.data_ptr(),
+              ws.numel(), _hip.stream())
     ref = oracle.linear_bf16(X, W) + (R if resid else 0)
     np.testing.assert_allclose(n(Y), ref, **BF_TOL)
+    if resid != "alias":  # fixed accumulation order: a second call is bit-identical
+        Y2 = torch.empty_like(Y)
+        _hip.call("ezops_gemm_bf16", Xg.data_ptr(), K, Wg.data_ptr(), Y2.data_ptr(), N,
+                  Rg.data_ptr() if resid else None, M, N, K, ws.data_ptr(), ws.numel(), _hip.stream())
+        assert torch.equal(Y, Y2)
 
 
 def _prefill_ref(op, data, paged):
