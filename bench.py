@@ -108,12 +108,9 @@ def layer_workload(torch, batch: int):
 
 
 def layer_bytes(batch: int, lens) -> int:
-    """Algorithmic bytes of one layer step: weights once, KV read over kv_lens, activations, new KV."""
-    HS, IS, H, Hkv, D = 4096, 12288, 32, 8, 128
-    weights = ((H + 2 * Hkv) * D * HS + HS * H * D + 2 * IS * HS + HS * IS) * 2  # 385,875,968
-    kv = 2 * Hkv * D * 2 * sum(lens)
-    act = batch * HS * 2 * 2 + batch * 2 * Hkv * D * 2
-    return weights + kv + act
+    from ezops import workloads
+
+    return workloads.layer_bytes(batch, lens)
 
 
 def decode_step(torch, data, lens, batch: int, steps: int, warmup: int, flush) -> dict:

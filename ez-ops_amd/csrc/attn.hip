@@ -246,7 +246,7 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
   constexpr int NSUB = kTile / 16;    // sub-tiles per tile
   constexpr int NDB = D / 16;         // 16-dim blocks of O^T
   constexpr int VI = kTile * D / 8 / kWave;  // 16-byte V loads per lane and tile
-  static_assert(G <= 8, "group size");
+  static_assert(G <= 16, "group size: one MFMA column per query head");
   static_assert(kTile == 32 && NDB % 4 == 0, "tile geometry");
 
   __shared__ __align__(16) uint16_t Vs[W][kTile * D];  // per-wave V tile (vswz layout)
@@ -600,7 +600,7 @@ struct SplitPlan {
 SplitPlan plan_splits(int64_t B, int64_t Hkv, int64_t Lh, int64_t G, bool balance = true) {
   const int64_t units = B * Hkv;
   const int64_t cus = num_cus();
-  // 8-wave blocks for few units; group 8 keeps 4 waves (its accumulators need
+  // 8-wave blocks for few units; groups 8 and 16 keep 4 waves (its accumulators need
   // the register budget of one wave per SIMD).
   const int waves = (units * 4 <= cus && G <= 4) ? 8 : 4;
   const int64_t target = waves == 8 ? 2 * cus : EZ_ATTN_TARGET4 * cus;  // blocks in flight
@@ -625,7 +625,9 @@ void launch_d(const AttnArgs& a, const SplitPlan& pl, float* opart, float* ml, i
   const dim3 grid{unsigned(a.B * a.Hkv * pl.nsplit), 1, 1}, block{unsigned(pl.waves * kWave), 1, 1};
 #define EZ_LAUNCH(GG, WW) \
   hipLaunchKernelGGL((attn_split_kernel<D, GG, WW, LAYER, PAGED>), grid, block, 0, s, a, pl.nsplit, opart, ml)
-  if (G == 8) {
+  if (G == 16) {
+    EZ_LAUNCH(16, 4);
+  } else if (G == 8) {
     EZ_LAUNCH(8, 4);
   } else if (pl.waves == 8) {
     if (G == 1) EZ_LAUNCH(1, 8);
@@ -655,7 +657,8 @@ int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
   EZ_REQUIRE(a.B * a.Hkv * kMaxSplits < (int64_t(1) << 31), "attn_decode: too many (batch, kv head) units");
   EZ_REQUIRE(a.H % a.Hkv == 0, "attn_decode: num_heads must be divisible by num_kv_heads");
   const int64_t G = a.H / a.Hkv;
-  EZ_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "attn_decode: group size %lld not in {1,2,4,8}", (long long)G);
+  EZ_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8 || G == 16, "attn_decode: group size %lld not in {1,2,4,8,16}",
+             (long long)G);
   EZ_REQUIRE(a.D == 64 || a.D == 128, "attn_decode: head_dim must be 64 or 128");
   EZ_REQUIRE((a.cos == nullptr) == (a.sin == nullptr), "attn_decode: cos and sin go together");
   EZ_REQUIRE(a.Lh >= 0, "attn_decode: max_kv_len must be >= 0");

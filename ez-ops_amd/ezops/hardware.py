@@ -181,6 +181,35 @@ def load_profile(name_or_path: str | Path = "mi355x") -> dict:
     return prof
 
 
+def compute_sol(roofline, profile: dict, input_bytes: int) -> dict | None:
+    """Speed-of-light times of one op call (the reference benches' rule,
+    benchmarks/bench_gemv.py:62-86): compute time at the calibrated tf32
+    tensor-core rate (the fp32 MFMA peak on gfx950), memory time of the
+    inputs at the calibrated HBM rate ("fused": the op reads each input
+    once) and of every ``_ref_forward`` intermediate ("unfused"); the
+    theoretical minimum is the larger of compute and fused memory.  None when
+    the profile lacks an HBM or tf32 peak.  Times in µs, ``theo_min_s`` in s."""
+    hbm = profile.get("hbm", {})
+    tc = profile.get("tensor_core", {}).get("tf32")
+    if not hbm.get("theoretical") or not tc or not tc.get("theoretical"):
+        return None
+    bw = float(hbm["theoretical"]) * float(hbm.get("calibration", 1.0))
+    fl = float(tc["theoretical"]) * float(tc.get("calibration", 1.0))
+    t_c, t_m = roofline.flops / fl, input_bytes / bw
+    t_min = max(t_c, t_m)
+    return {"compute_us": t_c * 1e6, "mem_fused_us": t_m * 1e6, "mem_unfused_us": roofline.bytes / bw * 1e6,
+            "theo_min_us": t_min * 1e6, "theo_min_s": t_min}
+
+
+def device_profile() -> dict | None:
+    """The loaded profile of GPU 0 (None for a device without one)."""
+    import torch
+
+    props = torch.cuda.get_device_properties(0)
+    key = detect_profile(props.name, getattr(props, "gcnArchName", ""))
+    return load_profile(key) if key else None
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description="Generate the MI355X roofline profile YAML")
     ap.add_argument("--output-dir", default=str(ASSETS))

@@ -19,8 +19,8 @@ class AttnDecodeHipKernel(BaseKernel):
         num_kv_heads = num_heads if num_kv_heads is None else num_kv_heads
         if num_heads % num_kv_heads:
             raise ValueError(f"num_heads ({num_heads}) must be divisible by num_kv_heads ({num_kv_heads})")
-        if num_heads // num_kv_heads not in (1, 2, 4, 8):
-            raise ValueError(f"GQA group size {num_heads // num_kv_heads} not supported (1, 2, 4 or 8)")
+        if num_heads // num_kv_heads not in (1, 2, 4, 8, 16):
+            raise ValueError(f"GQA group size {num_heads // num_kv_heads} not supported (1, 2, 4, 8 or 16)")
         if head_dim not in (64, 128):
             raise ValueError(f"head_dim ({head_dim}) must be 64 or 128")
         if batch < 1 or seq_len < 1:

@@ -16,8 +16,8 @@ from ..base_kernel import BaseKernel
 class PagedAttnDecodeHipKernel(BaseKernel):
     def __init__(self, batch: int, num_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
                  max_pages: int, num_pages: int):
-        if num_heads % num_kv_heads or num_heads // num_kv_heads not in (1, 2, 4, 8):
-            raise ValueError(f"GQA group size {num_heads}/{num_kv_heads} not supported (1, 2, 4 or 8)")
+        if num_heads % num_kv_heads or num_heads // num_kv_heads not in (1, 2, 4, 8, 16):
+            raise ValueError(f"GQA group size {num_heads}/{num_kv_heads} not supported (1, 2, 4, 8 or 16)")
         if head_dim not in (64, 128):
             raise ValueError(f"head_dim ({head_dim}) must be 64 or 128")
         if page_size < 32 or page_size & (page_size - 1):

@@ -1,14 +1,16 @@
 """Kernel timer (reference behaviour: ezops/ops/utils/bench.py:24-150).
 
 Protocol: warm up, capture the call into a HIP graph (eager fallback), then
-``n_trials`` trials of ``n_repeat`` event-timed replays, each preceded by a
-cache flush outside the timed region; the result is the median trial mean in
-milliseconds.
+``n_trials`` trials of ``n_repeat`` timed calls, each preceded by a cache
+flush; the result is the median trial mean in milliseconds.  How the calls
+are timed differs from the reference (``bench_kernel``'s ``method``): the
+default times the flush+call graph against the flush-only graph, because an
+event pair per call costs ~13 µs on MI355X.
 
 MI355X difference: the reference sizes its flush buffer to
 ``L2_cache_size``.  Here L2 is 4 MB per XCD but the 256 MB Infinity Cache
 (MALL) sits behind it, so a weight of a few hundred MB would stay resident
-and the measured GB/s would be inflated.  The flush writes 1 GiB, four times
+and the measured GB/s would be inflated.  The flush covers 1 GiB, four times
 the MALL.  The flush *reads* the buffer (a sum kernel): a write flush would
 leave the MALL full of dirty lines whose write-back then competes with the
 kernel being timed.
@@ -38,6 +40,25 @@ def flush_cache() -> None:
               _hip.stream())
 
 
+def _capture(body):
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        body()
+    torch.cuda.synchronize()
+    return g
+
+
+def _span_ms(run, n: int) -> float:
+    """GPU time of ``n`` back-to-back ``run()`` calls between one event pair."""
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(n):
+        run()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b)
+
+
 def bench_kernel(
     fn: Callable,
     args: tuple[Any, ...] = (),
@@ -46,36 +67,63 @@ def bench_kernel(
     n_trials: int = 3,
     flush: bool = True,
     use_graph: bool = True,
+    method: str = "diff",
 ) -> float:
-    """Median-of-trials mean latency of ``fn(*args)`` in ms."""
+    """Median-of-trials mean latency of ``fn(*args)`` in ms, caches cold.
+
+    ``method="diff"`` (default): one graph holds the flush and the call, a
+    second the flush alone; a trial times ``n_repeat`` back-to-back replays
+    of each between one event pair and returns the difference / n_repeat.
+    On MI355X an event pair around nothing reads ~5 µs and a graph replay
+    timed alone ~7 µs more (ROCm 7, measured), so the reference's
+    per-call event pairs put a ~13 µs floor under every op; in the
+    difference both costs appear on each side and cancel, leaving the
+    call's own GPU time plus its one dispatch gap.
+    ``method="events"``: the reference protocol as written (an event pair
+    around each replay, flush outside it), floor included.
+    Graph capture falls back to eager calls, with a warning."""
     for _ in range(n_warmup):
         if flush:
             flush_cache()
         fn(*args)
     torch.cuda.synchronize()
+    if not flush:
+        method = "events"
 
-    graph = None
+    call = lambda: fn(*args)  # noqa: E731
+    both = lambda: (flush_cache(), fn(*args))  # noqa: E731
+    run1, run0, run = both, flush_cache, call
     if use_graph:
         try:
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                fn(*args)
-            torch.cuda.synchronize()
-            graph = g
+            g = _capture(call)
+            run = g.replay
+            if method == "diff":
+                g1, g0 = _capture(both), _capture(flush_cache)
+                run1, run0 = g1.replay, g0.replay
         except Exception as e:  # not capturable: time eagerly, say so
-            graph = None
+            run, run1, run0 = call, both, flush_cache
             print(f"warning: graph capture failed for {getattr(fn, '__name__', fn)!r} "
                   f"({type(e).__name__}: {e}); timing eager launches")
-    run = graph.replay if graph is not None else (lambda: fn(*args))
-    if graph is not None:
-        for _ in range(n_warmup):
-            if flush:
-                flush_cache()
-            run()
-        torch.cuda.synchronize()
+    for _ in range(n_warmup):
+        if flush:
+            flush_cache()
+        run()
+        if method == "diff":
+            run1()
+            run0()
+    torch.cuda.synchronize()
 
     means = []
-    for _ in range(n_trials):
+    for t in range(n_trials):
+        if method == "diff":
+            if t % 2:
+                t0 = _span_ms(run0, n_repeat)
+                t1 = _span_ms(run1, n_repeat)
+            else:
+                t1 = _span_ms(run1, n_repeat)
+                t0 = _span_ms(run0, n_repeat)
+            means.append((t1 - t0) / n_repeat)
+            continue
         starts = [torch.cuda.Event(enable_timing=True) for _ in range(n_repeat)]
         ends = [torch.cuda.Event(enable_timing=True) for _ in range(n_repeat)]
         for i in range(n_repeat):

@@ -99,6 +99,11 @@ def config_f1(B: int, device="cuda", gen_device=None, S=32768):
     return pos, q, k, v, qw, kw, cos, sin, K, V
 
 
+def config_f1_positions(B: int, device="cuda", gen_device=None, S=32768) -> list[int]:
+    """F1's positions alone (the configuration's first draw, same values as ``config_f1``)."""
+    return _Gen(3, device, gen_device).randint(0, S, B)
+
+
 def config_f2(B: int, device="cuda", gen_device=None):
     """F2: attn [B, 4096], residual [B, 4096], Wo [4096, 4096], post_norm_w [4096]
     ~ N(1, 0.1), Wg, Wu [12288, 4096], Wd [4096, 12288] (weights ~ N(0, 0.02)),
@@ -114,6 +119,27 @@ def config_l_lens(B: int) -> list[int]:
     return torch.randint(1024, SEQ_MAX_L + 1, (B,), generator=g).tolist()
 
 
+def layer_bytes(batch: int, lens, hidden: int = 4096, inter: int = 12288, heads: int = 32, kv_heads: int = 8,
+                head_dim: int = 128) -> int:
+    """Algorithmic bytes of one Qwen3 decode-layer step (Qwen3-8B by default):
+    every weight once, K and V over ``lens``, the hidden row in and out and the
+    decoded token's k/v written."""
+    qkv = (heads + 2 * kv_heads) * head_dim
+    weights = (qkv * hidden + hidden * heads * head_dim + 3 * inter * hidden) * 2  # 385,875,968 at 8B
+    kv = 2 * kv_heads * head_dim * 2 * sum(lens)
+    act = batch * hidden * 2 * 2 + batch * 2 * kv_heads * head_dim * 2
+    return weights + kv + act
+
+
+def layer_op(B: int, backend="hip", **op_kw):
+    """L's layer op: Qwen3-8B, weighted norms, RoPE theta 1e6, 16384-row cache,
+    kv_lens from ``config_l_lens``."""
+    from .ops.qwen3_dense_decode import Qwen3DenseDecodeOp
+
+    return Qwen3DenseDecodeOp(B, SEQ_MAX_L, backend=backend, kv_lens=config_l_lens(B), norm_weights=True,
+                              rope_theta=1e6, **QWEN3_8B, **op_kw)
+
+
 def config_l(B: int, device="cuda", gen_device=None, backend="hip", **op_kw):
     """L: (op, data, lens) -- the Qwen3-8B layer op (weighted norms, RoPE theta
     1e6, 16384-row cache, kv_lens from ``config_l_lens``) and its forward
@@ -122,11 +148,9 @@ def config_l(B: int, device="cuda", gen_device=None, backend="hip", **op_kw):
     [24576, 4096], Wd [4096, 12288] ~ N(0, 0.02), then the input, q, k and
     post-attention norm weights ~ N(1, 0.1); the RoPE tables follow."""
     from .ops.fused_qk_norm_rope import rope_tables
-    from .ops.qwen3_dense_decode import Qwen3DenseDecodeOp
 
     lens = config_l_lens(B)
-    op = Qwen3DenseDecodeOp(B, SEQ_MAX_L, backend=backend, kv_lens=lens, norm_weights=True, rope_theta=1e6,
-                            **QWEN3_8B, **op_kw)
+    op = layer_op(B, backend, **op_kw)
     r = _Gen(4, device, gen_device)
     HS, IS, D = 4096, 12288, 128
     data = [r.normal(B, HS), r.normal(B, 8, SEQ_MAX_L, D), r.normal(B, 8, SEQ_MAX_L, D),

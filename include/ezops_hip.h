@@ -99,7 +99,7 @@ int ezops_reduce_sum_f32(const float* A, float* Out, int64_t n, void* workspace,
 
 /* Split-KV GQA decode attention, one query token per sequence.
  * Q [B, H, D] (== [B, H, 1, D]), K/V [B, Hkv, S, D], Out [B, H, D]; bf16.
- * H % Hkv == 0, H / Hkv in {1, 2, 4, 8}, D in {64, 128}.  kv_lens [B] int32 (NULL = S
+ * H % Hkv == 0, H / Hkv in {1, 2, 4, 8, 16}, D in {64, 128}.  kv_lens [B] int32 (NULL = S
  * for every sequence) limits sequence b to slots [0, kv_lens[b]).
  * max_kv_len: the caller's bound on the kv_lens entries (0 = S), used to plan
  * the split-KV grid and to request the first K/V tiles before the lengths
@@ -201,7 +201,7 @@ int ezops_o_proj_ffn_bf16(const void* attn, const void* residual, const void* Wo
 
 /* One Qwen3 dense decoder-layer decode step (see ezops/ops/qwen3_dense_decode.py).
  * The attention stage has the limits of ezops_attn_decode_bf16: H / Hkv in
- * {1, 2, 4, 8} and D in {64, 128} (EZOPS_EINVAL otherwise); the same holds
+ * {1, 2, 4, 8, 16} and D in {64, 128} (EZOPS_EINVAL otherwise); the same holds
  * for the paged layer and the multi-layer step below.
  * Replaces: Qwen3DenseDecodeOp backends (ezops/kernels/qwen3_dense_decode/
  * qwen3_dense_decode_triton.py:273-384, qwen3_dense_decode_persistent_tl.py:566-609). */

@@ -106,7 +106,8 @@ def _layer(batch, seq_len, kwargs, **mode):
         assert torch.equal(Vc[b][:, mask], V0[b][:, mask])
 
 
-@pytest.mark.parametrize("batch,seq_len,num_kv_heads", [(1, 128, 8), (1, 1000, 8), (2, 1025, 8), (1, 4096, 4), (1, 1, 8)])
+@pytest.mark.parametrize("batch,seq_len,num_kv_heads", [(1, 128, 8), (1, 1000, 8), (2, 1025, 8), (1, 4096, 4), (1, 1, 8),
+                                                                    (2, 1000, 1)])
 def test_qwen3_dense_decode_reference_mode(batch, seq_len, num_kv_heads):
     _layer(batch, seq_len, {**QWEN3_VL_2B, "num_kv_heads": num_kv_heads})
 

@@ -134,6 +134,8 @@ def test_reduce_unaligned_view():
     (2, 16, 8, 1025, 128, False),
     (3, 8, 8, 300, 64, False),     # MHA, head_dim 64
     (2, 32, 4, 4097, 128, False),  # group 8
+    (1, 16, 1, 32768, 128, False), # group 16: one kv head for 16 query heads (all MFMA columns live)
+    (3, 32, 2, 1500, 64, True),    # group 16, head_dim 64, ragged
     (4, 32, 8, 8192, 128, True),   # ragged lengths
     (3, 16, 8, 700, 64, True),
 ])
@@ -153,7 +155,7 @@ def test_attn_decode(B, H, Hkv, S, D, ragged):
     assert torch.equal(out, out2)
 
 
-@pytest.mark.parametrize("H,Hkv,D", [(32, 8, 128), (16, 16, 64), (32, 4, 128)])
+@pytest.mark.parametrize("H,Hkv,D", [(32, 8, 128), (16, 16, 64), (32, 4, 128), (16, 1, 128)])
 def test_attn_decode_tile_residues_and_nonfinite_tail(H, Hkv, D):
     """Every length residue modulo the 32-position tile (1, 31, 33, ...), with
     NaN / Inf in every cache row at or past the length: those rows are never

@@ -29,6 +29,7 @@ def n(x):
     (3, 16, 8, 64, 128, 9, 27),
     (16, 32, 8, 128, 256, 16, 256),  # B=16 at 4K capacity
     (2, 32, 4, 128, 1024, 3, 8),     # group 8, pages larger than a split chunk
+    (2, 16, 1, 128, 64, 40, 100),    # group 16
 ])
 def test_paged_equals_contiguous(B, H, Hkv, D, P, M, NP):
     torch.manual_seed(B * 100 + P)
