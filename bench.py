@@ -379,6 +379,10 @@ def profile_only(torch, _hip, flush, args) -> int:
     prefill: one Qwen3-8B layer prefill over a fresh 4096-token prompt.
     gemv:    the config-G GEMV (4096 x 4096 bf16, 33,570,816 algorithmic bytes).
     attn_a:  the config-A GQA decode (B=32, 32/8 heads, S=8192; 1,074,266,112 bytes).
+    burst:   the one-shot read roofline of the B=1 layer's stages: the streaming
+             (non-temporal) read probe over 50.3, 38.05, 33.57, 201.4 and 100.7 MB
+             (QKV, attention K/V, o_proj, gate/up, down), 10 cold dispatches each,
+             in that order.
     """
     if args.profile_kernel in ("gemv", "attn_a"):
         from ezops import AttnDecodeOp, GemvOp, workloads
@@ -404,6 +408,14 @@ def profile_only(torch, _hip, flush, args) -> int:
         for _ in range(10):
             flush()
             op(*data)
+    elif args.profile_kernel == "burst":
+        buf = torch.zeros(int(201.4e6) // 4 + 16, device="cuda")
+        sink = torch.zeros(16, device="cuda")
+        for nbytes in (50_331_648, 38_050_816, 33_570_816, 201_367_552, 100_663_296):
+            n = nbytes // 16 * 4
+            for _ in range(10):
+                flush()
+                _hip.call("ezops_hbm_probe", 4, sink.data_ptr(), buf.data_ptr(), None, n, 0.0, _hip.stream())
     elif args.profile_kernel == "copy":  # no flush in between: every probe dispatch is a 256 MiB copy
         n = (256 << 20) // 4
         a = torch.empty(n, device="cuda")
@@ -440,7 +452,7 @@ def main() -> int:
     ap.add_argument("--no-step", action="store_true", help="skip the 36-layer decode-step timing")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill timings")
     ap.add_argument("--batch", type=int, default=1, help="layer batch (headline is 1)")
-    ap.add_argument("--profile-kernel", choices=["gate_up", "copy", "layer", "prefill", "gemv", "attn_a"],
+    ap.add_argument("--profile-kernel", choices=["gate_up", "copy", "layer", "prefill", "gemv", "attn_a", "burst"],
                     help="only launch this kernel 10x between read flushes (for rocprofv3 counter runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

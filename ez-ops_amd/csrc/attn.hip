@@ -171,41 +171,45 @@ __device__ __forceinline__ void vt_read4(const uint32_t* addr, i32x2_t (&r)[8]) 
 }
 
 // Qwen3 per-head RMSNorm (fp32 statistics, weight) + half-split RoPE of one
-// bf16 head at `src`, rounded once to bf16 into `dst`.  One wave; lane l owns
-// the pairs (i, i + D/2), i = l, l + 64, ...  Operation order follows the
-// reference (ezops/ops/fused_qk_norm_rope.py:138-147).
+// bf16 head, rounded once to bf16.  One wave; lane l < D/2 owns the pair
+// (l, l + D/2).  Split in two so the kernel can request the inputs before
+// its first K/V tile (a wave's loads complete in order, so anything
+// requested after 16 KB of tile loads waits for them) and finish once they
+// have arrived.  Operation order follows the reference
+// (ezops/ops/fused_qk_norm_rope.py:138-147); a missing weight is 1 (exact).
+struct HeadIn {
+  uint16_t x1, x2, w1, w2;  // raw bf16: converting would wait for the loads here
+};
 template <int D>
-__device__ __forceinline__ void norm_rope_head(const uint16_t* src, const uint16_t* w, const uint16_t* crow,
-                                               const uint16_t* srow, float eps, uint16_t* dst, int lane) {
-  constexpr int HALF = D / 2;
-  constexpr int NP = (HALF + kWave - 1) / kWave;
-  float x1[NP], x2[NP];
-  float ss = 0.f;
-#pragma unroll
-  for (int t = 0; t < NP; ++t) {
-    const int i = lane + t * kWave;
-    x1[t] = i < HALF ? bf2f(src[i]) : 0.f;
-    x2[t] = i < HALF ? bf2f(src[i + HALF]) : 0.f;
-    ss += x1[t] * x1[t] + x2[t] * x2[t];
+__device__ __forceinline__ HeadIn load_head(const uint16_t* src, const uint16_t* w, int lane) {
+  static_assert(D <= 2 * kWave, "one pair per lane");
+  const int l = lane & (D / 2 - 1);  // lanes past D/2 repeat a pair (unused)
+  return HeadIn{src[l], src[l + D / 2], w[l], w[l + D / 2]};
+}
+struct RopeIn {
+  uint16_t c1, c2, s1, s2;
+};
+template <int D>
+__device__ __forceinline__ RopeIn load_rope(const uint16_t* crow, const uint16_t* srow, int lane) {
+  const int l = lane & (D / 2 - 1);
+  return RopeIn{crow[l], crow[l + D / 2], srow[l], srow[l + D / 2]};
+}
+template <int D>
+__device__ __forceinline__ void finish_head(const HeadIn& in, const RopeIn& ro, bool weighted, bool rope, float eps,
+                                            uint16_t* dst, int lane) {
+  const bool own = lane < D / 2;
+  const float x1 = own ? bf2f(in.x1) : 0.f, x2 = own ? bf2f(in.x2) : 0.f;
+  const float r = rsqrtf(wave_reduce_uniform<false>(x1 * x1 + x2 * x2) / float(D) + eps);
+  if (!own) return;
+  const float w1 = weighted ? bf2f(in.w1) : 1.f, w2 = weighted ? bf2f(in.w2) : 1.f;
+  const float y1 = __fmul_rn(__fmul_rn(x1, r), w1), y2 = __fmul_rn(__fmul_rn(x2, r), w2);
+  float o1 = y1, o2 = y2;
+  if (rope) {
+    o1 = __fadd_rn(__fmul_rn(y1, bf2f(ro.c1)), __fmul_rn(-y2, bf2f(ro.s1)));
+    o2 = __fadd_rn(__fmul_rn(y2, bf2f(ro.c2)), __fmul_rn(y1, bf2f(ro.s2)));
   }
-  const float r = rsqrtf(wave_reduce_uniform<false>(ss) / float(D) + eps);
-#pragma unroll
-  for (int t = 0; t < NP; ++t) {
-    const int i = lane + t * kWave;
-    if (i >= HALF) break;
-    float y1 = __fmul_rn(x1[t], r), y2 = __fmul_rn(x2[t], r);
-    if (w) {
-      y1 = __fmul_rn(y1, bf2f(w[i]));
-      y2 = __fmul_rn(y2, bf2f(w[i + HALF]));
-    }
-    float o1 = y1, o2 = y2;
-    if (crow) {
-      o1 = __fadd_rn(__fmul_rn(y1, bf2f(crow[i])), __fmul_rn(-y2, bf2f(srow[i])));
-      o2 = __fadd_rn(__fmul_rn(y2, bf2f(crow[i + HALF])), __fmul_rn(y1, bf2f(srow[i + HALF])));
-    }
-    dst[i] = f2bf(o1);
-    dst[i + HALF] = f2bf(o2);
-  }
+  dst[lane] = f2bf(o1);
+  dst[lane + D / 2] = f2bf(o2);
 }
 
 // Output element (query head hq = b*H + h, dim d): row-major [B, H*D], or the
@@ -316,6 +320,33 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
 
   int64_t t0 = (int64_t(split) * W + wave) * kTile;
   uint4 kn[VI], vn[VI];
+
+  // Layer prologue inputs, requested ahead of the first tile and without
+  // branches (a branch join would make the compiler wait for them there):
+  // this wave's query heads (h = wave, wave + W, ...; clamped), the k head and
+  // v row that split 0's last wave publishes (every wave requests them), and,
+  // once the length has arrived (a scalar load), the cos / sin rows of its
+  // position.  Absent weights or tables read the q row instead (unused).
+  constexpr int NQ = LAYER ? (G + W - 1) / W : 1;
+  const bool publisher = LAYER && split == 0 && wave == W - 1;
+  HeadIn qin[NQ], kin{};
+  RopeIn rin{};
+  uint16_t vv1 = 0, vv2 = 0;
+  if constexpr (LAYER) {
+    const uint16_t* row = a.qkv + int64_t(b) * a.qkv_bs;
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      const int h = wave + j * W < G ? wave + j * W : G - 1;
+      qin[j] = load_head<D>(row + (h0 + h) * D, a.qw ? a.qw : row, lane);
+    }
+    kin = load_head<D>(row + a.H * D + int64_t(kvh) * D, a.kw ? a.kw : row, lane);
+    const uint16_t* vrow = row + (a.H + a.Hkv) * D + int64_t(kvh) * D;
+    vv1 = vrow[lane & (D / 2 - 1)];
+    vv2 = vrow[(lane & (D / 2 - 1)) + D / 2];
+    int64_t pos = int64_t(a.kv_lens ? Lraw : int32_t(a.S)) - 1;
+    pos = pos < 0 ? 0 : (pos >= a.Lh ? a.Lh - 1 : pos);  // the address only; L = 0 writes nothing
+    rin = load_rope<D>(a.cos ? a.cos + pos * D : row, a.sin ? a.sin + pos * D : row, lane);
+  }
   __builtin_amdgcn_sched_barrier(0);
   {
     const int64_t ts = tile_start(t0, a.Lh - 1);
@@ -336,17 +367,17 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
   bf16x8_t qf[NS];
   if constexpr (LAYER) {
     const int64_t pos = L - 1;
-    const bool publisher = split == 0 && wave == W - 1;
     if (L > 0) {
-      const uint16_t* row = a.qkv + int64_t(b) * a.qkv_bs;
-      const uint16_t* crow = a.cos ? a.cos + pos * D : nullptr;
-      const uint16_t* srow = a.sin ? a.sin + pos * D : nullptr;
-      for (int h = wave; h < G; h += W)
-        norm_rope_head<D>(row + (h0 + h) * D, a.qw, crow, srow, a.eps, &Qs[h][0], lane);
+      const bool rope = a.cos != nullptr;
+#pragma unroll
+      for (int j = 0; j < NQ; ++j)
+        if (wave + j * W < G) finish_head<D>(qin[j], rin, a.qw != nullptr, rope, a.eps, &Qs[wave + j * W][0], lane);
       if (publisher) {
-        norm_rope_head<D>(row + a.H * D + int64_t(kvh) * D, a.kw, crow, srow, a.eps, Kn, lane);
-        const uint16_t* vrow = row + (a.H + a.Hkv) * D + int64_t(kvh) * D;
-        for (int i = lane; i < D; i += kWave) Vn[i] = vrow[i];
+        finish_head<D>(kin, rin, a.kw != nullptr, rope, a.eps, Kn, lane);
+        if (lane < D / 2) {
+          Vn[lane] = vv1;
+          Vn[lane + D / 2] = vv2;
+        }
       }
     }
     __syncthreads();  // Qs, Kn, Vn complete
