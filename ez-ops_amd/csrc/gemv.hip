@@ -177,8 +177,10 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_valu_kernel(LinearArgs a) {
 //   C:            C[4g + j][i]      -> weight row row0 + 4g + j, batch m0 + i
 // A register of the A operand spans 16 weight rows, so loading it straight
 // from HBM reads 64-byte pieces of 16 rows per instruction.  Instead the
-// load unit lands each chunk in LDS (global_load_lds_dwordx4) with 512-byte
-// row-contiguous reads, at 16-byte slot (r, c ^ r) for piece c of row r; the
+// load unit lands each chunk in LDS (buffer_load_dwordx4 ... lds; the wave
+// index is uniform, so the LDS destination needs no per-instruction
+// readfirstlane) with 512-byte row-contiguous reads, at 16-byte slot
+// (r, c ^ r) for piece c of row r; the
 // A fragments are then ds_read_b128 with no bank conflicts (the 16 lanes of
 // a read hit 16 distinct slot columns).  Every wave owns a two-stage ring of
 // such tiles, so the loop has no block barrier.  X fragments (L2-resident
@@ -236,7 +238,7 @@ __global__ __launch_bounds__(NW * kWave) void linear_mfma_kernel(LinearArgs a) {
   __shared__ __align__(16) uint4 Wl1[NW][T][kMfmaSlices][kWave];
   __shared__ float red[NW][T][4][kWave];
 
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int i = lane & 15, g = lane >> 4;
   const int64_t m0 = int64_t(blockIdx.y) * 16;
   const int64_t m = m0 + i;
@@ -245,16 +247,23 @@ __global__ __launch_bounds__(NW * kWave) void linear_mfma_kernel(LinearArgs a) {
   // DMA lane roles: slice q of a chunk holds rows 2q, 2q+1 (lanes 0-31, 32-63);
   // lane piece cs = lane & 31 stores the row's 16-byte piece cs ^ r.
   const int dr = lane >> 5, cs = lane & 31;
-  const uint16_t* wrow[T][kMfmaSlices];
+  // Buffer resources over the tile's rows (reads past them return zeros)
+  // and per-lane byte offsets within the tile; the chunk's K offset is the
+  // scalar offset of the load.
+  __amdgpu_buffer_rsrc_t wres0, wres1;  // (an array of resources drops the kernel's host stub)
+  uint32_t woff[kMfmaSlices];
   auto set_rows = [&](int64_t r0) {
+    const int64_t rows = a.N - r0 < 16 ? a.N - r0 : 16;
+    wres0 = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.W + r0 * a.K), 0, int(rows * a.K * 2),
+                                              0x00020000);
+    wres1 = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>((SILU ? a.W2 : a.W) + r0 * a.K), 0,
+                                              int(rows * a.K * 2), 0x00020000);
 #pragma unroll
-    for (int t = 0; t < T; ++t)
-#pragma unroll
-      for (int q = 0; q < kMfmaSlices; ++q) {
-        int64_t row = r0 + 2 * q + dr;
-        if (row >= a.N) row = a.N - 1;
-        wrow[t][q] = ((SILU && t == 1) ? a.W2 : a.W) + row * a.K;
-      }
+    for (int q = 0; q < kMfmaSlices; ++q) {
+      int64_t row = 2 * q + dr;
+      if (r0 + row >= a.N) row = a.N - 1 - r0;
+      woff[q] = uint32_t((row * a.K + int64_t(cs ^ (2 * q + dr)) * 8) * 2);
+    }
   };
   set_rows(row0);
   // Rows past M read row 0: their outputs are never stored.
@@ -264,17 +273,13 @@ __global__ __launch_bounds__(NW * kWave) void linear_mfma_kernel(LinearArgs a) {
   const int64_t cb = nchunks * wave / NW, ce = nchunks * (wave + 1) / NW;
 
   auto dma = [&](int64_t c, uint4 (*stage)[kMfmaSlices][kWave]) {
-    const int64_t k0 = c * kMfmaKC;
+    const uint32_t k0b = uint32_t(c * kMfmaKC * 2);  // past K: the next row's weights or zeros, zeroed at use
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
-      for (int q = 0; q < kMfmaSlices; ++q) {
-        const int r = 2 * q + dr;
-        int64_t k = k0 + int64_t(cs ^ r) * 8;
-        k = k < a.K ? k : a.K - 8;  // past K: real weights, zeroed at use
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>(wrow[t][q] + k),
-                                         (__attribute__((address_space(3))) void*)(&stage[t][q][0]), 16, 0, 0);
-      }
+      for (int q = 0; q < kMfmaSlices; ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(t ? wres1 : wres0, (__attribute__((address_space(3))) void*)(&stage[t][q][0]),
+                                                 16, woff[q], k0b, 0, 0);
   };
   // Unconditional loads from clamped addresses: no branch around a pending load.
   // Packed X: the fragment of (batch block, k-step) is 1 KiB at a fixed place.
