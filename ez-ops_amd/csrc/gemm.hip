@@ -5,29 +5,40 @@
 // Both operands are K-contiguous rows, the layout of activations [tokens,
 // features] and of weights [out, in].
 //
-// Block tile 256 x 256, K-steps of 64; 8 waves (2 per SIMD), wave (wm, wn)
-// owning rows 128 wm .. +127 and columns 64 wn .. +63 of the tile: 4 x 2
+// Block tile 256 x 256, K-steps of 64; 8 waves (2 per SIMD), wave (g, wn)
+// owning rows 128 g .. +127 and columns 64 wn .. +63 of the tile: 4 x 2
 // v_mfma_f32_32x32x16_bf16 accumulators (128 fp32 per lane).  Operand layout
 // of the 32x32x16 MFMA: lane 32h + i holds A[i][8h .. 8h+7] and
 // B[8h .. 8h+7][i]; reg r of lane 32h + j holds C[8(r/4) + 4h + r%4][j].  With
 // A = X rows and B[k][n] = W[n][k], both operands are 16-byte pieces of K-rows.
 //
+// Ping-pong schedule: the two waves of a SIMD belong to the two row groups
+// (g = 0: waves 0-3, g = 1: waves 4-7) and run the same code, group 1 one
+// block barrier behind, so in every interval between barriers one group
+// reads a whole K-step's fragments from LDS (24 ds_read_b128 into 96 VGPRs)
+// while the other issues that K-step's 32 MFMAs from registers; the matrix
+// pipe of each SIMD is fed by one wave at a time with nothing to wait for.
+// (With both waves reading and multiplying in step, a double-buffered
+// version ran at 0.7 of this.)
+//
 // The X and W tiles of a K-step (256 rows x 128 bytes each) land in LDS by
-// DMA (buffer_load_dwordx4 ... lds: no staging registers; the per-lane
-// offsets are computed once and the K offset rides in a scalar register, so
-// issuing a K-step's DMA costs no vector address arithmetic), double-
-// buffered, one barrier per K-step.  Rows are stored with their 16-byte
-// chunks XOR-swizzled by (row >> 1) & 7: gfx950's LDS is 64 banks (256
-// bytes) wide, and a 16-lane phase of a fragment read (16 consecutive
-// 128-byte rows) then covers all 16 bank groups (SQ_LDS_BANK_CONFLICT 0; the
-// swizzle by row & 7 measured 50% conflict cycles).  The DMA reads the
-// global chunk that belongs at each fixed LDS slot.
-// Fragment reads are asm blocks: the compiler would otherwise wait for the
-// next tile's DMA (vmcnt 0) in front of every LDS read.  The reads of K-step
-// s + 1 are issued before the MFMAs of step s and waited for after them
-// (scheduling barriers keep that order; without them the compiler hoisted
-// the MFMAs above the reads and reused their registers, serialising every
-// step).
+// DMA (buffer_load_dwordx4 ... lds: no staging registers; per-lane offsets
+// computed once, the K offset and the 32-row stride in a scalar register),
+// in two stages.  Issuing a K-step's 64 KiB costs the CU's address unit
+// ~1000 cycles, so it is split: group 0 issues X of step j + 1 after its
+// reads of step j (into the other stage, which both groups have finished),
+// group 1 issues W of step j + 2 after its reads of step j (the stage both
+// groups have just finished).  Each group waits for its own DMA before the
+// barrier that precedes the first read of that step; issuing all of it from
+// group 0 left the MFMA pipes idle while group 0's reads waited behind it
+// (0.8x).  Rows are stored with their 16-byte chunks XOR-swizzled by
+// (row >> 1) & 7: gfx950's LDS is 64 banks (256 bytes) wide, and a 16-lane
+// phase of a fragment read (16 consecutive 128-byte rows) then covers all 16
+// bank groups (SQ_LDS_BANK_CONFLICT 0).  The DMA reads the global chunk that
+// belongs at each fixed LDS slot; rows past M / N lie past the end of the
+// tile's buffer resource and read zeros (never stored).  Fragment reads are
+// asm blocks: the compiler would otherwise wait for outstanding DMA (vmcnt 0)
+// in front of every LDS read.
 //
 // Tiles are dealt to the XCDs in contiguous ranges (block b runs on XCD b % 8)
 // and, within a range, in groups of 8 M-tiles (M fastest inside a group), so
@@ -47,7 +58,7 @@ constexpr int kGWaves = 8;
 constexpr int kGThreads = kGWaves * kWave;
 constexpr int kGRowBytes = kGK * 2;                      // 128 bytes per tile row
 constexpr int kGTileBytes = kGM * kGRowBytes;            // 32 KiB per operand tile
-constexpr int kGDma = kGTileBytes / 16 / kGThreads;      // 16-byte DMA loads per thread and operand tile
+constexpr int kGDma = kGTileBytes / 16 / (kGThreads / 2);  // 16-byte DMA loads per thread of one group and tile
 constexpr int kGroupM = 8;                                // M-tiles per tile group
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4v_t __attribute__((ext_vector_type(4)));
@@ -61,11 +72,10 @@ struct GemmArgs {
   int tm, tn;  // tiles along M and N
 };
 
-// Fragment reads of one K-step (16 k): 4 A pieces (the wave's 4 row tiles)
-// and 2 B pieces (its 2 column tiles).  frag_issue starts them; frag_wait
-// waits for them and, taking the fragments as operands, keeps every use
-// after the wait.
-__device__ __forceinline__ void frag_issue(const uint32_t (&addr)[6], u32x4v_t (&r)[6]) {
+// Fragment reads of one 16-k substep: 4 A pieces (the wave's 4 row tiles)
+// and 2 B pieces (its 2 column tiles); frag_wait waits for a K-step's 24
+// and, taking them as operands, keeps every use after the wait.
+__device__ __forceinline__ void frag_issue(const uint32_t (&addr)[6], u32x4v_t* r) {
   asm volatile(
       "ds_read_b128 %0, %6\n\t"
       "ds_read_b128 %1, %7\n\t"
@@ -76,14 +86,21 @@ __device__ __forceinline__ void frag_issue(const uint32_t (&addr)[6], u32x4v_t (
       : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5])
       : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]), "v"(addr[5]));
 }
-__device__ __forceinline__ void frag_wait(u32x4v_t (&r)[6]) {
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]));
+__device__ __forceinline__ void frag_wait(u32x4v_t (&f)[24]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]), "+v"(f[7]),
+                 "+v"(f[8]), "+v"(f[9]), "+v"(f[10]), "+v"(f[11]), "+v"(f[12]), "+v"(f[13]), "+v"(f[14]),
+                 "+v"(f[15]), "+v"(f[16]), "+v"(f[17]), "+v"(f[18]), "+v"(f[19]), "+v"(f[20]), "+v"(f[21]),
+                 "+v"(f[22]), "+v"(f[23]));
 }
 
 __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) void gemm_bf16_kernel(GemmArgs a) {
   EZ_PROF_WAVE(kProfGemm);
-  __shared__ __align__(16) uint16_t As[2][kGM * kGK];
-  __shared__ __align__(16) uint16_t Bs[2][kGN * kGK];
+  // Two stages of X and W tiles; after the K loop the same 128 KiB holds the
+  // block's C tile in bf16 (16 KiB per wave) for row-contiguous stores.
+  __shared__ __align__(16) uint16_t lds[2 * (kGM + kGN) * kGK];
+  uint16_t(*As)[kGM * kGK] = reinterpret_cast<uint16_t(*)[kGM * kGK]>(&lds[0]);
+  uint16_t(*Bs)[kGN * kGK] = reinterpret_cast<uint16_t(*)[kGN * kGK]>(&lds[2 * kGM * kGK]);
 
   // tile of this block: XCD-contiguous ranges, groups of kGroupM M-tiles
   const int ntiles = a.tm * a.tn;
@@ -93,44 +110,40 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) 
   const int gm = a.tm - grp * kGroupM < kGroupM ? a.tm - grp * kGroupM : kGroupM;
   const int64_t m0 = int64_t(grp * kGroupM + gi % gm) * kGM, n0 = int64_t(gi / gm) * kGN;
 
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
-  const int wm = wave >> 2, wn = wave & 3;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar LDS destinations
+  const int g = wave >> 2, wn = wave & 3, wg = wave & 3;  // row group, column slot, wave within the group
   const int h = lane >> 5, i = lane & 31;
 
-  // DMA sources: load c of wave w fills LDS chunks p = (c * 8 + w) * 64 + lane
-  // (row p / 8, slot p % 8), which holds the row's logical chunk
-  // slot ^ ((row >> 1) & 7); byte offsets from the operand base.
-  const int wv = __builtin_amdgcn_readfirstlane(wave);  // uniform: LDS destinations in scalar registers
-  uint32_t aoff[kGDma], boff[kGDma];
+  // DMA: load c of group wave wg fills LDS chunk p = (c * 4 + wg) * 64 + lane,
+  // tile row 32 c + 8 wg + lane / 8, slot lane % 8, which holds the row's
+  // logical chunk slot ^ ((row >> 1) & 7).  The per-lane offset does not
+  // depend on c (32 c rows go in the scalar offset).
+  const int dr = 8 * wg + (lane >> 3), lc = (lane & 7) ^ ((dr >> 1) & 7);
+  const uint32_t aoff = uint32_t((dr * a.ldx + lc * 8) * 2), boff = uint32_t((dr * a.K + lc * 8) * 2);
+  const int64_t mrows = a.M - m0 < kGM ? a.M - m0 : kGM, nrows = a.N - n0 < kGN ? a.N - n0 : kGN;
+  const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.X + m0 * a.ldx), 0, int(((mrows - 1) * a.ldx + a.K) * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.W + n0 * a.K), 0, int(nrows * a.K * 2), 0x00020000);
+  auto dma_x = [&](int64_t k0, int buf) {
 #pragma unroll
-  for (int c = 0; c < kGDma; ++c) {
-    const int p = (c * kGWaves + wave) * kWave + lane;
-    const int r = p >> 3, lc = (p & 7) ^ ((r >> 1) & 7);
-    const int64_t xr = m0 + r < a.M ? m0 + r : a.M - 1;  // tail rows: a valid row, never stored
-    const int64_t wr = n0 + r < a.N ? n0 + r : a.N - 1;
-    aoff[c] = uint32_t((xr * a.ldx + lc * 8) * 2);
-    boff[c] = uint32_t((wr * a.K + lc * 8) * 2);
-  }
-  const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.X), 0, 0x7fffffff,
-                                                                        0x00020000);
-  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.W), 0, 0x7fffffff,
-                                                                        0x00020000);
-  auto dma = [&](int64_t k0, int buf) {
+    for (int c = 0; c < kGDma; ++c)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (__attribute__((address_space(3))) void*)(&As[buf][(c * 4 + wg) * kWave * 8]),
+                                               16, aoff, uint32_t((k0 + int64_t(c) * 32 * a.ldx) * 2), 0, 0);
+  };
+  auto dma_w = [&](int64_t k0, int buf) {
 #pragma unroll
-    for (int c = 0; c < kGDma; ++c) {
-      const int slot = (c * kGWaves + wv) * kWave * 8;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (__attribute__((address_space(3))) void*)(&As[buf][slot]), 16,
-                                               aoff[c], uint32_t(k0 * 2), 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, (__attribute__((address_space(3))) void*)(&Bs[buf][slot]), 16,
-                                               boff[c], uint32_t(k0 * 2), 0, 0);
-    }
+    for (int c = 0; c < kGDma; ++c)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, (__attribute__((address_space(3))) void*)(&Bs[buf][(c * 4 + wg) * kWave * 8]),
+                                               16, boff, uint32_t((k0 + int64_t(c) * 32 * a.K) * 2), 0, 0);
   };
 
-  // Fragment addresses (bytes within a tile): A row 128 wm + 32 ra + i, B row
-  // 64 wn + 32 rb + i; K-step s reads logical chunk 2s + h.
+  // Fragment addresses (bytes within a tile): A row 128 g + 32 ra + i, B row
+  // 64 wn + 32 rb + i; substep s reads logical chunk 2s + h.
   uint32_t arow[4], brow[2];
 #pragma unroll
-  for (int ra = 0; ra < 4; ++ra) arow[ra] = uint32_t(128 * wm + 32 * ra + i);
+  for (int ra = 0; ra < 4; ++ra) arow[ra] = uint32_t(128 * g + 32 * ra + i);
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) brow[rb] = uint32_t(64 * wn + 32 * rb + i);
   const uint32_t abase[2] = {
@@ -148,63 +161,117 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) 
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[ra][rb][r] = 0.f;
 
-  const int64_t nk = a.K / kGK;
-  dma(0, 0);
-  wait_vm<0>();
-  __syncthreads();
-  for (int64_t kt = 0; kt < nk; ++kt) {
-    const int buf = int(kt & 1);
-    if (kt + 1 < nk) dma((kt + 1) * kGK, buf ^ 1);  // next K-step's tiles land while this one is multiplied
-    auto frag_addr = [&](int s, uint32_t (&addr)[6]) {
+  u32x4v_t fr[24];  // one K-step: fr[6 s + ra] A pieces, fr[6 s + 4 + rb] B pieces
+  auto read_step = [&](int buf) {
+#pragma unroll
+    for (int s = 0; s < kGK / 16; ++s) {
+      uint32_t addr[6];
 #pragma unroll
       for (int ra = 0; ra < 4; ++ra)
         addr[ra] = abase[buf] + arow[ra] * kGRowBytes + (((2 * s + h) ^ ((arow[ra] >> 1) & 7)) << 4);
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb)
         addr[4 + rb] = bbase[buf] + brow[rb] * kGRowBytes + (((2 * s + h) ^ ((brow[rb] >> 1) & 7)) << 4);
-    };
-    u32x4v_t f[2][6];
-    uint32_t addr[6];
-    frag_addr(0, addr);
-    frag_issue(addr, f[0]);
+      frag_issue(addr, &fr[6 * s]);
+    }
+    frag_wait(fr);
+  };
+  auto mult_step = [&]() {
 #pragma unroll
-    for (int s = 0; s < kGK / 16; ++s) {
-      frag_wait(f[s & 1]);
-      if (s + 1 < kGK / 16) {
-        frag_addr(s + 1, addr);
-        frag_issue(addr, f[(s + 1) & 1]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
+    for (int s = 0; s < kGK / 16; ++s)
 #pragma unroll
       for (int ra = 0; ra < 4; ++ra)
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
-          acc[ra][rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f[s & 1][ra]),
-                                                                __builtin_bit_cast(bf16x8_t, f[s & 1][4 + rb]),
+          acc[ra][rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, fr[6 * s + ra]),
+                                                                __builtin_bit_cast(bf16x8_t, fr[6 * s + 4 + rb]),
                                                                 acc[ra][rb], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    wait_vm<0>();     // the next tiles have landed ...
-    __syncthreads();  // ... and every wave is done with this buffer
-  }
+  };
+  auto barrier = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  };
 
-  // epilogue: reg r of lane (h, j = i) is Y[row0 + 8(r/4) + 4h + r%4][col0 + i]
+  const int64_t nk = a.K / kGK;
+  // Steps 0 and 1 in flight before the loop (group 1 owns W of step 1).
+  if (g == 0) {
+    dma_x(0, 0);
+    dma_w(0, 0);
+  } else if (nk > 1) {
+    dma_w(kGK, 1);
+  }
+  wait_vm<0>();
+  __syncthreads();
+  if (g == 1) barrier();  // group 1 runs one interval behind
+  for (int64_t j = 0; j < nk; ++j) {
+    const int buf = int(j & 1);
+    read_step(buf);
+    if (g == 0) {
+      if (j + 1 < nk) dma_x((j + 1) * kGK, buf ^ 1);
+    } else if (j + 2 < nk) {
+      dma_w((j + 2) * kGK, buf);
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vm<kGDma>();  // W of step j + 1 (the older loads)
+    } else {
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vm<0>();
+    }
+    barrier();
+    mult_step();
+    if (g == 0 && j + 1 < nk) {
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vm<0>();  // X of step j + 1
+    }
+    barrier();
+  }
+  if (g == 0) barrier();  // the same barrier count for both groups
+
+  // Epilogue.  Reg r of lane (h, i) in acc[ra][rb] is C[32 ra + 8(r/4) + 4h +
+  // r%4][32 rb + i] of the wave's 128 x 64 tile: rounded to bf16 into the
+  // wave's LDS slot (row-major, 128 bytes a row), then read back 16 bytes a
+  // lane (8 rows per instruction) for 16-byte stores and residual loads.
+  __syncthreads();  // every wave is done with the operand tiles
+  uint16_t* ct = &lds[wave * 128 * 64];
 #pragma unroll
   for (int ra = 0; ra < 4; ++ra)
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      const int64_t col = n0 + 64 * wn + 32 * rb + i;
-      const int64_t row0 = m0 + 128 * wm + 32 * ra + 4 * h;
-      if (col >= a.N) continue;
+    for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = row0 + 8 * (r >> 2) + (r & 3);
-        if (row >= a.M) continue;
-        uint16_t* y = a.Y + row * a.ldy + col;
-        const float v = acc[ra][rb][r];
-        *y = a.R ? f2bf(bf2f(a.R[row * a.ldy + col]) + round_bf(v)) : f2bf(v);
+      for (int r = 0; r < 16; ++r)
+        ct[(32 * ra + 8 * (r >> 2) + 4 * h + (r & 3)) * 64 + 32 * rb + i] = f2bf(acc[ra][rb][r]);
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's writes are in LDS before its reads
+  const bool vec = a.ldy % 8 == 0 && (reinterpret_cast<uintptr_t>(a.Y) & 15) == 0 &&
+                   (!a.R || (reinterpret_cast<uintptr_t>(a.R) & 15) == 0);
+  const int lr = lane >> 3, lcb = (lane & 7) * 8;
+#pragma unroll 4
+  for (int q = 0; q < 16; ++q) {
+    const int rr = 8 * q + lr;
+    const int64_t row = m0 + 128 * g + rr, col = n0 + 64 * wn + lcb;
+    if (row >= a.M || col >= a.N) continue;
+    const uint4 cv = *reinterpret_cast<const uint4*>(&ct[rr * 64 + lcb]);
+    uint16_t* y = a.Y + row * a.ldy + col;
+    if (vec && col + 8 <= a.N) {
+      uint4 out = cv;
+      if (a.R) {
+        const uint4 rv = *reinterpret_cast<const uint4*>(a.R + row * a.ldy + col);
+        const uint32_t* c32 = reinterpret_cast<const uint32_t*>(&cv);
+        const uint32_t* r32 = reinterpret_cast<const uint32_t*>(&rv);
+        uint32_t* o32 = reinterpret_cast<uint32_t*>(&out);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = __uint_as_float(r32[e] << 16) + __uint_as_float(c32[e] << 16);
+          const float hi = __uint_as_float(r32[e] & 0xffff0000u) + __uint_as_float(c32[e] & 0xffff0000u);
+          o32[e] = uint32_t(f2bf(lo)) | (uint32_t(f2bf(hi)) << 16);
+        }
       }
+      *reinterpret_cast<uint4*>(y) = out;
+    } else {
+      const uint16_t* c16 = reinterpret_cast<const uint16_t*>(&cv);
+      for (int e = 0; e < 8 && col + e < a.N; ++e)
+        y[e] = a.R ? f2bf(bf2f(a.R[row * a.ldy + col + e]) + bf2f(c16[e])) : c16[e];
     }
+  }
 }
 
 }  // namespace
