@@ -340,8 +340,14 @@ extern "C" int ezops_qwen3_prefill_bf16(const ezops_qwen3_layer* p, int64_t T, c
   rc = launch_prefill_attn(a, s);
   if (!rc) rc = gemm_bf16(w.att, QR, W(p->Wo), w.h, HS, hidden, T, HS, QR, w.gemm_ws, kGemmWorkspace, s);
   if (!rc) rc = ezops_rmsnorm_bf16(w.h, p->post_norm_w, w.xn, T, HS, p->eps, s);
-  if (!rc) rc = gemm_bf16(w.xn, HS, W(p->Wgu), w.gu, 2 * IS, nullptr, T, 2 * IS, HS, w.gemm_ws, kGemmWorkspace, s);
-  if (!rc) rc = launch_silu_mul(w.gu, w.act, T, IS, s);
+  if (!rc) {
+    if (gemm_swiglu_supported(w.xn, HS, W(p->Wgu), w.act, IS, T, IS, HS)) {
+      rc = gemm_swiglu(w.xn, HS, W(p->Wgu), w.act, IS, T, IS, HS, s);
+    } else {
+      rc = gemm_bf16(w.xn, HS, W(p->Wgu), w.gu, 2 * IS, nullptr, T, 2 * IS, HS, w.gemm_ws, kGemmWorkspace, s);
+      if (!rc) rc = launch_silu_mul(w.gu, w.act, T, IS, s);
+    }
+  }
   if (!rc)
     rc = gemm_bf16(w.act, IS, W(p->Wd), static_cast<uint16_t*>(p->out), HS, w.h, T, HS, IS, w.gemm_ws,
                    kGemmWorkspace, s);

@@ -70,6 +70,7 @@ struct GemmArgs {
   const uint16_t* R;
   int64_t M, N, K;
   int tm, tn;  // tiles along M and N
+  int64_t IS;  // SwiGLU mode: rows [0, IS) of W are gate, [IS, 2 IS) up; Y is [M, IS]
 };
 
 // Fragment reads of one 16-k substep: 4 A pieces (the wave's 4 row tiles)
@@ -94,6 +95,12 @@ __device__ __forceinline__ void frag_wait(u32x4v_t (&f)[24]) {
                  "+v"(f[22]), "+v"(f[23]));
 }
 
+// SWIGLU: the tile's 256 W rows are gate rows n0 .. n0 + 127 and the up rows
+// IS + n0 .. +127 of the same features (n0 = 128 x tile column), and the
+// epilogue writes silu(gate) * up for those 128 features: the prefill's
+// SwiGLU without the [M, 2 IS] intermediate.  Rounding as the separate pass:
+// gate and up rounded to bf16, the activation rounded, the product rounded.
+template <bool SWIGLU>
 __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) void gemm_bf16_kernel(GemmArgs a) {
   EZ_PROF_WAVE(kProfGemm);
   // Two stages of X and W tiles; after the K loop the same 128 KiB holds the
@@ -108,7 +115,7 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) 
   if (ntiles % 8 == 0) t = (t % 8) * (ntiles / 8) + t / 8;
   const int grp = t / (kGroupM * a.tn), gi = t % (kGroupM * a.tn);
   const int gm = a.tm - grp * kGroupM < kGroupM ? a.tm - grp * kGroupM : kGroupM;
-  const int64_t m0 = int64_t(grp * kGroupM + gi % gm) * kGM, n0 = int64_t(gi / gm) * kGN;
+  const int64_t m0 = int64_t(grp * kGroupM + gi % gm) * kGM, n0 = int64_t(gi / gm) * (SWIGLU ? kGN / 2 : kGN);
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar LDS destinations
@@ -125,7 +132,10 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) 
   const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(a.X + m0 * a.ldx), 0, int(((mrows - 1) * a.ldx + a.K) * 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(a.W + n0 * a.K), 0, int(nrows * a.K * 2), 0x00020000);
+      const_cast<uint16_t*>(a.W + n0 * a.K), 0, int((SWIGLU ? kGN / 2 : nrows) * a.K * 2), 0x00020000);
+  // SwiGLU: tile rows 128 .. 255 (DMA loads c >= kGDma / 2) come from the up block
+  const __amdgpu_buffer_rsrc_t ures = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.W + (SWIGLU ? a.IS + n0 : 0) * a.K), 0, int(kGN / 2 * a.K * 2), 0x00020000);
   auto dma_x = [&](int64_t k0, int buf) {
 #pragma unroll
     for (int c = 0; c < kGDma; ++c)
@@ -134,9 +144,13 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) 
   };
   auto dma_w = [&](int64_t k0, int buf) {
 #pragma unroll
-    for (int c = 0; c < kGDma; ++c)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, (__attribute__((address_space(3))) void*)(&Bs[buf][(c * 4 + wg) * kWave * 8]),
-                                               16, boff, uint32_t((k0 + int64_t(c) * 32 * a.K) * 2), 0, 0);
+    for (int c = 0; c < kGDma; ++c) {
+      const bool up = SWIGLU && c >= kGDma / 2;
+      const int cr = up ? c - kGDma / 2 : c;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(up ? ures : wres,
+                                               (__attribute__((address_space(3))) void*)(&Bs[buf][(c * 4 + wg) * kWave * 8]),
+                                               16, boff, uint32_t((k0 + int64_t(cr) * 32 * a.K) * 2), 0, 0);
+    }
   };
 
   // Fragment addresses (bytes within a tile): A row 128 g + 32 ra + i, B row
@@ -240,6 +254,32 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) 
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         ct[(32 * ra + 8 * (r >> 2) + 4 * h + (r & 3)) * 64 + 32 * rb + i] = f2bf(acc[ra][rb][r]);
+  if constexpr (SWIGLU) {
+    // Wave (g, wn) of the group finalises rows 128 g + 32 wn .. +31 of the
+    // 128 features; gate column c of the tile lives in wave (g, c / 64), up
+    // column c in wave (g, 2 + c / 64).
+    __syncthreads();
+    for (int q = 0; q < 8; ++q) {
+      const int rr = 32 * wn + 4 * q + (lane >> 4), cc = (lane & 15) * 8;  // row in the group, feature
+      const int64_t row = m0 + 128 * g + rr;
+      if (row >= a.M) continue;
+      const uint16_t* gp = &lds[(4 * g + (cc >> 6)) * 128 * 64 + rr * 64 + (cc & 63)];
+      const uint4 gv = *reinterpret_cast<const uint4*>(gp);
+      const uint4 uv = *reinterpret_cast<const uint4*>(gp + 2 * 128 * 64);
+      const uint32_t* g32 = reinterpret_cast<const uint32_t*>(&gv);
+      const uint32_t* u32 = reinterpret_cast<const uint32_t*>(&uv);
+      uint4 out;
+      uint32_t* o32 = reinterpret_cast<uint32_t*>(&out);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a0 = round_bf(silu(__uint_as_float(g32[e] << 16)));
+        const float a1 = round_bf(silu(__uint_as_float(g32[e] & 0xffff0000u)));
+        o32[e] = pack_bf2(a0 * __uint_as_float(u32[e] << 16), a1 * __uint_as_float(u32[e] & 0xffff0000u));
+      }
+      *reinterpret_cast<uint4*>(a.Y + row * a.ldy + n0 + cc) = out;
+    }
+    return;
+  }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's writes are in LDS before its reads
   const bool vec = a.ldy % 8 == 0 && (reinterpret_cast<uintptr_t>(a.Y) & 15) == 0 &&
                    (!a.R || (reinterpret_cast<uintptr_t>(a.R) & 15) == 0);
@@ -290,9 +330,25 @@ bool gemm_mfma_supported(const uint16_t* X, int64_t ldx, const uint16_t* W, cons
 int gemm_mfma(const uint16_t* X, int64_t ldx, const uint16_t* W, uint16_t* Y, int64_t ldy, const uint16_t* R,
               int64_t M, int64_t N, int64_t K, hipStream_t s) {
   EZ_REQUIRE(gemm_mfma_supported(X, ldx, W, Y, ldy, R, M, N, K), "gemm: shape or alignment not supported by the MFMA kernel");
-  GemmArgs a{X, ldx, W, Y, ldy, R, M, N, K, int((M + kGM - 1) / kGM), int((N + kGN - 1) / kGN)};
-  hipLaunchKernelGGL(gemm_bf16_kernel, dim3(unsigned(a.tm * a.tn)), dim3(kGThreads), 0, s, a);
+  GemmArgs a{X, ldx, W, Y, ldy, R, M, N, K, int((M + kGM - 1) / kGM), int((N + kGN - 1) / kGN), 0};
+  hipLaunchKernelGGL(gemm_bf16_kernel<false>, dim3(unsigned(a.tm * a.tn)), dim3(kGThreads), 0, s, a);
   return launch_status("gemm (MFMA)");
+}
+
+bool gemm_swiglu_supported(const uint16_t* X, int64_t ldx, const uint16_t* W, const uint16_t* Y, int64_t ldy,
+                           int64_t M, int64_t IS, int64_t K) {
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  return IS % (kGN / 2) == 0 && ldy % 8 == 0 && al16(Y) && ldy >= IS &&
+         gemm_mfma_supported(X, ldx, W, Y, ldy, nullptr, M, 2 * IS, K);
+}
+
+int gemm_swiglu(const uint16_t* X, int64_t ldx, const uint16_t* W, uint16_t* Y, int64_t ldy, int64_t M, int64_t IS,
+                int64_t K, hipStream_t s) {
+  EZ_REQUIRE(gemm_swiglu_supported(X, ldx, W, Y, ldy, M, IS, K),
+             "gemm_swiglu: shape or alignment not supported (IS % 128, K % 64, 16-byte rows)");
+  GemmArgs a{X, ldx, W, Y, ldy, nullptr, M, 2 * IS, K, int((M + kGM - 1) / kGM), int(IS / (kGN / 2)), IS};
+  hipLaunchKernelGGL(gemm_bf16_kernel<true>, dim3(unsigned(a.tm * a.tn)), dim3(kGThreads), 0, s, a);
+  return launch_status("gemm_swiglu (MFMA)");
 }
 
 }  // namespace ez

@@ -147,6 +147,12 @@ int gemm_bf16(const uint16_t* X, int64_t ldx, const uint16_t* W, uint16_t* Y, in
 
 extern "C" size_t ezops_gemm_workspace_size(void) { return ez::kGemmWorkspace; }
 
+extern "C" int ezops_gemm_swiglu_bf16(const void* X, int64_t ldx, const void* Wgu, void* Y, int64_t ldy, int64_t M,
+                                      int64_t IS, int64_t K, hipStream_t stream) {
+  return ez::gemm_swiglu(static_cast<const uint16_t*>(X), ldx, static_cast<const uint16_t*>(Wgu),
+                         static_cast<uint16_t*>(Y), ldy, M, IS, K, stream);
+}
+
 extern "C" int ezops_gemm_bf16(const void* X, int64_t ldx, const void* W, void* Y, int64_t ldy, const void* R,
                                int64_t M, int64_t N, int64_t K, void* ws, size_t ws_bytes, hipStream_t stream) {
   return ez::gemm_bf16(static_cast<const uint16_t*>(X), ldx, static_cast<const uint16_t*>(W),

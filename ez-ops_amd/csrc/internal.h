@@ -119,6 +119,12 @@ bool gemm_mfma_supported(const uint16_t* X, int64_t ldx, const uint16_t* W, cons
                          const uint16_t* R, int64_t M, int64_t N, int64_t K);
 int gemm_mfma(const uint16_t* X, int64_t ldx, const uint16_t* W, uint16_t* Y, int64_t ldy, const uint16_t* R,
               int64_t M, int64_t N, int64_t K, hipStream_t s);
+// Gate/up projection fused with SwiGLU: Y[M, IS] = silu(X Wg^T) * (X Wu^T),
+// W = [Wg; Wu] as [2 IS, K]; rounding as GEMM then the separate SwiGLU pass.
+bool gemm_swiglu_supported(const uint16_t* X, int64_t ldx, const uint16_t* W, const uint16_t* Y, int64_t ldy,
+                           int64_t M, int64_t IS, int64_t K);
+int gemm_swiglu(const uint16_t* X, int64_t ldx, const uint16_t* W, uint16_t* Y, int64_t ldy, int64_t M, int64_t IS,
+                int64_t K, hipStream_t s);
 
 // Library GEMM (hipBLASLt): Y[M,N] = X[M,K] W[N,K]^T (+ R, same layout as Y).
 constexpr size_t kGemmWorkspace = size_t(32) << 20;

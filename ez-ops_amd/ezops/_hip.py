@@ -58,6 +58,7 @@ SIGNATURES: dict[str, tuple] = {
     "ezops_qwen3_prefill_bf16": (_i32, [C.POINTER(Qwen3LayerParams), _i64, _p, _i64, _p, _i64, _i64, _p, _sz, _p]),
     "ezops_gemm_workspace_size": (_sz, []),
     "ezops_gemm_bf16": (_i32, [_p, _i64, _p, _p, _i64, _p, _i64, _i64, _i64, _p, _sz, _p]),
+    "ezops_gemm_swiglu_bf16": (_i32, [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p]),
     "ezops_paged_attn_decode_bf16": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                             _f32, _p, _sz, _p]),
     "ezops_qk_norm_rope_bf16": (_i32, [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p,

@@ -300,6 +300,16 @@ int ezops_gemm_bf16(const void* X, int64_t ldx, const void* W, void* Y, int64_t 
                     int64_t M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
                     hipStream_t stream);
 
+/* Prefill gate/up projection fused with SwiGLU:
+ * Y[M, IS] = bf16(bf16(silu(bf16(X Wg^T))) * bf16(X Wu^T)) with Wgu = [Wg; Wu]
+ * as [2 IS, K] (the layer's gate/up weight), bit-identical to
+ * ezops_gemm_bf16 into [M, 2 IS] followed by the SwiGLU pass.  Requires
+ * IS % 128 == 0, K % 64 == 0, ldx % 8 == 0, ldy % 8 == 0, ldy >= IS and
+ * 16-byte aligned X, Wgu, Y (EZOPS_EINVAL otherwise).
+ * No counterpart in the reference (its FFN is the decode GEMV chain). */
+int ezops_gemm_swiglu_bf16(const void* X, int64_t ldx, const void* Wgu, void* Y, int64_t ldy, int64_t M,
+                           int64_t IS, int64_t K, hipStream_t stream);
+
 /* Wave-level kernel timelines (a library built with -DEZ_PROFILE=1; the
  * production build returns EZOPS_ENOSYS).  Every wave of the instrumented
  * kernels (GEMV/GEMM, decode and prefill attention, combine, norms, softmax,

@@ -81,6 +81,41 @@ def test_gemm_vs_oracle(M, N, K, resid):
         assert torch.equal(Y, Y2)
 
 
+@pytest.mark.parametrize("M,IS,K", [(300, 384, 256), (512, 1024, 512), (257, 128, 64)])
+def test_gemm_swiglu_vs_unfused(M, IS, K):
+    """The fused gate/up + SwiGLU GEMM against the plain GEMM into [M, 2 IS]
+    followed by SwiGLU on the host (bf16 gate/up, bf16 activation, bf16
+    product): equal up to the device exp (1 bf16 ulp), bitwise repeatable."""
+    rng = np.random.default_rng(M + IS)
+    X = oracle.bf16(rng.standard_normal((M, K)).astype(np.float32))
+    W = oracle.bf16(rng.standard_normal((2 * IS, K)).astype(np.float32) * K ** -0.5)
+    g = lambda a: torch.from_numpy(a).to(torch.bfloat16).cuda()  # noqa: E731
+    Xg, Wg = g(X), g(W)
+    gu = torch.empty(M, 2 * IS, dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(_hip.size("ezops_gemm_workspace_size"), dtype=torch.uint8, device="cuda")
+    _hip.call("ezops_gemm_bf16", Xg.data_ptr(), K, Wg.data_ptr(), gu.data_ptr(), 2 * IS, None, M, 2 * IS, K,
+              ws.data_ptr(), ws.numel(), _hip.stream())
+    Y = torch.empty(M, IS, dtype=torch.bfloat16, device="cuda")
+    _hip.call("ezops_gemm_swiglu_bf16", Xg.data_ptr(), K, Wg.data_ptr(), Y.data_ptr(), IS, M, IS, K, _hip.stream())
+    gh = n(gu)
+    act = oracle.bf16(gh[:, :IS] / (1.0 + np.exp(-gh[:, :IS])))
+    ref = oracle.bf16(act * gh[:, IS:])
+    np.testing.assert_allclose(n(Y), ref, rtol=1e-2, atol=1e-2)
+    assert np.mean(n(Y) == ref) > 0.99  # all but exp-rounding ties are bit-equal
+    Y2 = torch.empty_like(Y)
+    _hip.call("ezops_gemm_swiglu_bf16", Xg.data_ptr(), K, Wg.data_ptr(), Y2.data_ptr(), IS, M, IS, K, _hip.stream())
+    assert torch.equal(Y, Y2)
+
+
+def test_gemm_swiglu_rejects_unsupported():
+    X = torch.zeros(16, 64, dtype=torch.bfloat16, device="cuda")
+    W = torch.zeros(2 * 96, 64, dtype=torch.bfloat16, device="cuda")
+    Y = torch.zeros(16, 96, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(RuntimeError, match="-22"):  # IS = 96 is not a multiple of 128: EINVAL
+        _hip.call("ezops_gemm_swiglu_bf16", X.data_ptr(), 64, W.data_ptr(), Y.data_ptr(), 96, 16, 96, 64,
+                  _hip.stream())
+
+
 def _prefill_ref(op, data, paged):
     npy = [n(x) for x in data]
     K0, V0 = npy[1], npy[2]

@@ -65,4 +65,5 @@ def test_wave_trace_prefill():
         out = op(*data)
     # the same kernels with the wave recorder compiled in: bit-identical results
     assert torch.equal(out, ref)
-    check_records(tr.records, {"rmsnorm_bf16", "gemm", "qk_norm_rope", "prefill_attn", "silu_mul"})
+    # (SwiGLU runs in the gate/up GEMM's epilogue at Qwen3-8B's IS = 12288)
+    check_records(tr.records, {"rmsnorm_bf16", "gemm", "qk_norm_rope", "prefill_attn"})
