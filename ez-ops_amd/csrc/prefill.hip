@@ -29,6 +29,7 @@ EZ_PROF_DEFINE(prefill)
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLazy = 8.f;        // log2 headroom of the lazily moved softmax max
 constexpr int kPD = 128;            // head dim
 constexpr int kPW = 8;              // waves per block: 2 per SIMD, all sharing the block's K/V tiles
 constexpr int kBK = 64;             // keys per tile
@@ -253,15 +254,21 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
       for (int kk = 0; kk < kBK / 32; ++kk)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[kk][r]);
-      mx = halves_max(mx);
-      const float mn = fmaxf(m, mx * sl2);  // finite: key 0 is visible to every query
-      const float alpha = __builtin_amdgcn_exp2f(m - mn);
-      m = mn;
-      l *= alpha;
-      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // rescale only when some row max moved
+      mx = halves_max(mx) * sl2;
+      // Lazy rescale: the reference max m moves (and O, l are rescaled) only
+      // when some row's tile max exceeds it by more than kLazy, so the
+      // probabilities stay <= 2^kLazy (exact in fp32, the same relative
+      // precision in the bf16 P operand) and most tiles skip the 64 rescale
+      // multiplies.  The first tile always sets m (m = -inf).
+      if (__builtin_amdgcn_ballot_w64(mx > m + kLazy)) {
+        const float mn = fmaxf(m, mx);  // finite: key 0 is visible to every query
+        const float alpha = __builtin_amdgcn_exp2f(m - mn);
+        m = mn;
+        l *= alpha;
 #pragma unroll
         for (int d = 0; d < kPD / 32; ++d) o[d] *= alpha;
       }
+      const float mn = m;
 #pragma unroll
       for (int kk = 0; kk < kBK / 32; ++kk) {
 #pragma unroll
