@@ -48,17 +48,6 @@ def _capture(body):
     return g
 
 
-def _span_ms(run, n: int) -> float:
-    """GPU time of ``n`` back-to-back ``run()`` calls between one event pair."""
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for _ in range(n):
-        run()
-    b.record()
-    torch.cuda.synchronize()
-    return a.elapsed_time(b)
-
-
 def bench_kernel(
     fn: Callable,
     args: tuple[Any, ...] = (),
@@ -72,13 +61,18 @@ def bench_kernel(
     """Median-of-trials mean latency of ``fn(*args)`` in ms, caches cold.
 
     ``method="diff"`` (default): one graph holds the flush and the call, a
-    second the flush alone; a trial times ``n_repeat`` back-to-back replays
-    of each between one event pair and returns the difference / n_repeat.
+    second the flush alone; a trial alternates ``n_repeat`` replays of each,
+    every replay between its own event pair, and returns the median of the
+    pairwise differences.
     On MI355X an event pair around nothing reads ~5 µs and a graph replay
     timed alone ~7 µs more (ROCm 7, measured), so the reference's
     per-call event pairs put a ~13 µs floor under every op; in the
     difference both costs appear on each side and cancel, leaving the
-    call's own GPU time plus its one dispatch gap.
+    call's own GPU time plus its one dispatch gap.  A cold kernel's own time
+    varies from launch to launch (the config-G GEMV: 6.9-10.3 µs per
+    dispatch in a kernel trace), so repeated calls of this timer spread by
+    about +-1 µs for kernels under ~10 µs; a profiler's kernel trace is the
+    precise figure there.
     ``method="events"``: the reference protocol as written (an event pair
     around each replay, flush outside it), floor included.
     Graph capture falls back to eager calls, with a warning."""
@@ -116,13 +110,20 @@ def bench_kernel(
     means = []
     for t in range(n_trials):
         if method == "diff":
-            if t % 2:
-                t0 = _span_ms(run0, n_repeat)
-                t1 = _span_ms(run1, n_repeat)
-            else:
-                t1 = _span_ms(run1, n_repeat)
-                t0 = _span_ms(run0, n_repeat)
-            means.append((t1 - t0) / n_repeat)
+            # (flush + call) and flush-alone replays alternate, each between
+            # its own event pair; a trial is the median of the pairwise
+            # differences, so clock drift between the two kinds cancels too
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(2 * n_repeat)]
+            for i in range(n_repeat):
+                for k, r in ((0, run1), (1, run0)) if (i + t) % 2 == 0 else ((1, run0), (0, run1)):
+                    a, b = ev[2 * i + k]
+                    a.record()
+                    r()
+                    b.record()
+            torch.cuda.synchronize()
+            d = sorted(ev[2 * i][0].elapsed_time(ev[2 * i][1]) - ev[2 * i + 1][0].elapsed_time(ev[2 * i + 1][1])
+                       for i in range(n_repeat))
+            means.append(d[len(d) // 2])
             continue
         starts = [torch.cuda.Event(enable_timing=True) for _ in range(n_repeat)]
         ends = [torch.cuda.Event(enable_timing=True) for _ in range(n_repeat)]
