@@ -67,20 +67,21 @@ typedef unsigned int u32x4v_t __attribute__((ext_vector_type(4)));
 // for the next tile's prefetch here; these reads touch the other buffer, and
 // the volatile asm keeps its place between the barriers that order them
 // against the DMA into that buffer.
+template <int OFF>
 __device__ __forceinline__ void lds_read8(const uint32_t (&addr)[8], u32x4v_t (&r)[8]) {
   asm volatile(
-      "ds_read_b128 %0, %8\n\t"
-      "ds_read_b128 %1, %9\n\t"
-      "ds_read_b128 %2, %10\n\t"
-      "ds_read_b128 %3, %11\n\t"
-      "ds_read_b128 %4, %12\n\t"
-      "ds_read_b128 %5, %13\n\t"
-      "ds_read_b128 %6, %14\n\t"
-      "ds_read_b128 %7, %15\n\t"
+      "ds_read_b128 %0, %8 offset:%16\n\t"
+      "ds_read_b128 %1, %9 offset:%16\n\t"
+      "ds_read_b128 %2, %10 offset:%16\n\t"
+      "ds_read_b128 %3, %11 offset:%16\n\t"
+      "ds_read_b128 %4, %12 offset:%16\n\t"
+      "ds_read_b128 %5, %13 offset:%16\n\t"
+      "ds_read_b128 %6, %14 offset:%16\n\t"
+      "ds_read_b128 %7, %15 offset:%16\n\t"
       "s_waitcnt lgkmcnt(0)"
       : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
       : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]), "v"(addr[5]), "v"(addr[6]),
-        "v"(addr[7]));
+        "v"(addr[7]), "i"(OFF));
 }
 static_assert(kPD / 16 == 8, "lds_read8 reads the 8 k-steps of a 128-dim key row");
 typedef int i32x2_t __attribute__((ext_vector_type(2)));
@@ -167,75 +168,104 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
   const uint16_t* kslab = a.K + (int64_t(b) * a.Hkv + kvh) * a.S * kPD;
   const uint16_t* vslab = a.V + (int64_t(b) * a.Hkv + kvh) * a.S * kPD;
   const int kend32 = int(kend);
-  // K and V go straight to LDS (global_load_lds_dwordx4): load c of wave w
+  // K and V go straight to LDS (16-byte LDS DMA loads): load c of wave w
   // fills LDS chunks 256c + 64w .. +63, one per lane, so lane tid writes
   // chunk p = 256c + tid = (key p/16, slot p%16) and reads the global chunk
   // slot ^ (key & 15) of K (conflict-free 16-byte reads of the S operand)
   // and slot ^ 4(key & 3) of V: the transposing reads of the V^T operand
   // take 4 keys x 64 bytes per 32 lanes, each key in its own 64-byte bank
   // block.
-  auto load_tile = [&](int64_t k0, int nb) {
-    const int k032 = int(k0);
+  // Contiguous cache: buffer loads over the slab's first kend rows (rows past
+  // them read as zeros, which the causal mask hides and which keep P.V
+  // finite), per-lane offsets fixed, the tile's row offset in a scalar.
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  __amdgpu_buffer_rsrc_t kres, vres;
+  uint32_t koff[kLPT], voff[kLPT];
+  if constexpr (!PAGED) {
+    kres = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kslab), 0, kend32 * kPD * 2, 0x00020000);
+    vres = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vslab), 0, kend32 * kPD * 2, 0x00020000);
 #pragma unroll
     for (int c = 0; c < kLPT; ++c) {
       const int id = tid + c * kPW * kWave;
       const int r = id >> 4;
-      const int row = min(k032 + r, kend32 - 1);
-      const int kc = (id & 15) ^ (r & 15), vc = (id & 15) ^ (4 * (r & 3));
-      const uint16_t *kp, *vp;
-      if constexpr (PAGED) {
-        kp = cache_row<PAGED>(a, a.K, b, kvh, row) + kc * 8;
-        vp = cache_row<PAGED>(a, a.V, b, kvh, row) + vc * 8;
-      } else {
-        kp = kslab + uint32_t(row * kPD + kc * 8);
-        vp = vslab + uint32_t(row * kPD + vc * 8);
+      koff[c] = uint32_t(r * kPD + (((id & 15) ^ (r & 15)) * 8)) * 2;
+      voff[c] = uint32_t(r * kPD + (((id & 15) ^ (4 * (r & 3))) * 8)) * 2;
+    }
+  }
+  auto load_tile = [&](int64_t k0, int nb) {
+    const int k032 = int(k0);
+    if constexpr (!PAGED) {
+#pragma unroll
+      for (int c = 0; c < kLPT; ++c) {
+        const int slot = (c * kPW + wave_u) * kWave * 8;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(kres, (__attribute__((address_space(3))) void*)(&Ks[nb][slot]), 16,
+                                                 koff[c], uint32_t(k032) * (kPD * 2), 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vres, (__attribute__((address_space(3))) void*)(&Vs[nb][slot]), 16,
+                                                 voff[c], uint32_t(k032) * (kPD * 2), 0, 0);
       }
-      const int slot = (c * kPW + wave) * kWave * 8;
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(kp),
-                                       (__attribute__((address_space(3))) void*)(&Ks[nb][slot]), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(vp),
-                                       (__attribute__((address_space(3))) void*)(&Vs[nb][slot]), 16, 0, 0);
+    } else {  // paged: rows through the block table, clamped to kend
+#pragma unroll
+      for (int c = 0; c < kLPT; ++c) {
+        const int id = tid + c * kPW * kWave;
+        const int r = id >> 4;
+        const int row = min(k032 + r, kend32 - 1);
+        const int kc = (id & 15) ^ (r & 15), vc = (id & 15) ^ (4 * (r & 3));
+        const uint16_t* kp = cache_row<PAGED>(a, a.K, b, kvh, row) + kc * 8;
+        const uint16_t* vp = cache_row<PAGED>(a, a.V, b, kvh, row) + vc * 8;
+        const int slot = (c * kPW + wave) * kWave * 8;
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(kp),
+                                         (__attribute__((address_space(3))) void*)(&Ks[nb][slot]), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(vp),
+                                         (__attribute__((address_space(3))) void*)(&Vs[nb][slot]), 16, 0, 0);
+      }
     }
   };
   load_tile(0, 0);
   wait_vm<0>();  // the first tile has landed before the barrier
   __syncthreads();
 
-  int buf = 0;
-  for (int64_t k0 = 0; k0 < kend; k0 += kBK, buf ^= 1) {
+  // Per-lane LDS addresses in buffer 0, fixed for the whole loop: K row
+  // 32kk + j has the swizzle of row j (32kk is a multiple of 16), so the
+  // key block, the buffer and the 16-key step are immediate offsets.
+  uint32_t kaddr[kPD / 16];
+#pragma unroll
+  for (int s = 0; s < kPD / 16; ++s)
+    kaddr[s] = uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint16_t*)(&Ks[0][0]))) +
+               uint32_t(j * kPD + (((2 * s + h) ^ (j & 15)) * 8)) * 2;
+  // V^T operand addresses: lane (i = 16(g%2) + m of 16-lane group g, half
+  // h) reads key row 4h + m/4 (+ 16-key step, + 8 for the second half),
+  // dims 32d + i - m%4 + 4(m%4) .. +3 = 32d + 16(g%2) + 4(m%4) .. +3.
+  uint32_t vaddr[kPD / 32];
+  {
+    const uint32_t vs_base =
+        uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint16_t*)(&Vs[0][0])));
+    const int mm = lane & 15, g1 = (lane >> 4) & 1;
+    const int vrow = 4 * h + (mm >> 2);
+#pragma unroll
+    for (int d = 0; d < kPD / 32; ++d) {
+      const int ch = 4 * d + 2 * g1 + ((mm & 3) >> 1);
+      vaddr[d] = vs_base + uint32_t(vrow * kPD * 2 + ((ch ^ (4 * (vrow & 3))) * 16) + (mm & 1) * 8);
+    }
+  }
+  constexpr uint32_t kBufBytes = kBK * kPD * 2;  // one K (or V) buffer
+  const bf16x2_t ones = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);
+
+  // One tile in LDS buffer BUF (a compile-time index: the loop below runs
+  // two tiles per iteration).
+  auto tile = [&](int64_t k0, auto bufc) {
+    constexpr int BUF = decltype(bufc)::value;
     const bool more = k0 + kBK < kend;
-    if (more) load_tile(k0 + kBK, buf ^ 1);  // next tile's global loads overlap this tile's math
+    if (more) load_tile(k0 + kBK, BUF ^ 1);  // next tile's global loads overlap this tile's math
 
     if (k0 <= wave_last) {  // a wave whose queries all precede the tile skips it
       f32x16_t st[kBK / 32];
-      const uint32_t ks_base =
-          uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint16_t*)(&Ks[buf][0])));
-      // V^T operand addresses: lane (i = 16(g%2) + m of 16-lane group g, half
-      // h) reads key row 4h + m/4 (+ 16-key step, + 8 for the second half),
-      // dims 32d + i - m%4 + 4(m%4) .. +3 = 32d + 16(g%2) + 4(m%4) .. +3.
-      uint32_t vaddr[kPD / 32];
-      {
-        const uint32_t vs_base =
-            uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint16_t*)(&Vs[buf][0])));
-        const int mm = lane & 15, g1 = (lane >> 4) & 1;
-        const int vrow = 4 * h + (mm >> 2);
-#pragma unroll
-        for (int d = 0; d < kPD / 32; ++d) {
-          const int ch = 4 * d + 2 * g1 + ((mm & 3) >> 1);
-          vaddr[d] = vs_base + uint32_t(vrow * kPD * 2 + ((ch ^ (4 * (vrow & 3))) * 16) + (mm & 1) * 8);
-        }
-      }
-      uint32_t kaddr[kPD / 16];
 #pragma unroll
       for (int kk = 0; kk < kBK / 32; ++kk) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) st[kk][r] = 0.f;
-        const int row = 32 * kk + j;  // key row read by this lane (A operand row i = j)
-#pragma unroll
-        for (int s = 0; s < kPD / 16; ++s)
-          kaddr[s] = ks_base + uint32_t(row * kPD + (((2 * s + h) ^ (row & 15)) * 8)) * 2;
         u32x4v_t kf[kPD / 16];
-        lds_read8(kaddr, kf);
+        if (kk == 0) lds_read8<BUF * kBufBytes>(kaddr, kf);
+        else lds_read8<BUF * kBufBytes + 32 * kPD * 2>(kaddr, kf);
 #pragma unroll
         for (int s = 0; s < kPD / 16; ++s)
           st[kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[s]), qf[s], st[kk], 0, 0, 0);
@@ -279,16 +309,17 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
           for (int q = 0; q < 4; ++q) {
             const float p0 = __builtin_amdgcn_exp2f(fmaf(st[kk][8 * u + 2 * q], sl2, -mn));
             const float p1 = __builtin_amdgcn_exp2f(fmaf(st[kk][8 * u + 2 * q + 1], sl2, -mn));
-            l += p0 + p1;
             w[q] = cvt_bf2(p0, p1);
+            // the denominator sums the bf16 weights the P.V product uses
+            l = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[q]), ones, l, false);
           }
           const bf16x8_t pb = as_bf16x8(make_uint4(w[0], w[1], w[2], w[3]));
           // keys 32kk + 16u + 4h + 0..3 and + 8..11 of dims 32d + j
           i32x2_t vf[2 * (kPD / 32)];
-          if (kk == 0 && u == 0) lds_read_vt4<0>(vaddr, vf);
-          else if (kk == 0) lds_read_vt4<16 * kPD * 2>(vaddr, vf);
-          else if (u == 0) lds_read_vt4<32 * kPD * 2>(vaddr, vf);
-          else lds_read_vt4<48 * kPD * 2>(vaddr, vf);
+          if (kk == 0 && u == 0) lds_read_vt4<BUF * kBufBytes>(vaddr, vf);
+          else if (kk == 0) lds_read_vt4<BUF * kBufBytes + 16 * kPD * 2>(vaddr, vf);
+          else if (u == 0) lds_read_vt4<BUF * kBufBytes + 32 * kPD * 2>(vaddr, vf);
+          else lds_read_vt4<BUF * kBufBytes + 48 * kPD * 2>(vaddr, vf);
 #pragma unroll
           for (int d = 0; d < kPD / 32; ++d) {
             const bf16x8_t va = __builtin_bit_cast(
@@ -301,6 +332,10 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
     }
     if (more) wait_vm<0>();  // the next tile's DMA has landed before the barrier
     __syncthreads();
+  };
+  for (int64_t k0 = 0; k0 < kend; k0 += 2 * kBK) {
+    tile(k0, std::integral_constant<int, 0>{});
+    if (k0 + kBK < kend) tile(k0 + kBK, std::integral_constant<int, 1>{});
   }
 
   // l: this lane's share of query j's sum; the two lane halves add up.
@@ -348,6 +383,7 @@ int launch_prefill_attn(const PrefillAttnArgs& a, hipStream_t s) {
   EZ_REQUIRE(a.Q && a.K && a.V && a.Out && a.cu, "prefill_attn: null pointer");
   EZ_REQUIRE(a.B >= 1 && a.T >= 0 && a.H >= 1 && a.Hkv >= 1 && a.S >= 1 && a.max_q >= 0, "prefill_attn: bad shape");
   EZ_REQUIRE(a.D == kPD, "prefill_attn: head_dim must be %d", kPD);
+  EZ_REQUIRE(a.S < (int64_t(1) << 23), "prefill_attn: cache capacity must be below 2^23 rows");
   EZ_REQUIRE(a.H % a.Hkv == 0, "prefill_attn: num_heads must be divisible by num_kv_heads");
   const int64_t G = a.H / a.Hkv;
   EZ_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "prefill_attn: GQA group size must be 1, 2, 4 or 8");
