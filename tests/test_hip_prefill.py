@@ -49,6 +49,40 @@ def test_prefill_attn_paged_equals_contiguous(page_size):
     assert torch.equal(out, cop(Q, K, V))
 
 
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_prefill_attn_nonfinite_cache_tail(paged):
+    """Cache rows past each sequence's last key (past + q_len) are never
+    weighted: NaN / Inf there leave the output bit-identical.  The lengths
+    end inside a 64-key tile, so the last tile straddles the written rows."""
+    torch.manual_seed(31)
+    q_lens, past = [100, 37], [5, 190]
+    B, S, ps = 2, 512, 64
+    kw = dict(page_size=ps, num_pages=B * S // ps) if paged else {}
+    op = PrefillAttnOp(B, 32, 8, 128, S, q_lens, past, backend="hip", **kw)
+    data = list(op.gen_data())
+    ref = op(*data)
+    K, V = data[1], data[2]
+    if paged:  # block_table[b, p] is the page holding rows p*ps .. p*ps + ps - 1 of sequence b
+        bt = data[3]
+        for b in range(B):
+            end = past[b] + q_lens[b]
+            for p in range(S // ps):
+                lo = max(end - p * ps, 0)
+                if lo < ps:
+                    pg = int(bt[b, p])
+                    K[pg, :, lo:] = float("nan")
+                    V[pg, :, lo:] = float("inf")
+    else:
+        for b in range(B):
+            end = past[b] + q_lens[b]
+            K[b, :, end:] = float("nan")
+            V[b, :, end:] = float("inf")
+    out = op(*data)
+    assert torch.isfinite(out.float()).all()
+    assert torch.equal(out, ref)
+
+
 # ---- prefill layer and its GEMM
 from ezops import Qwen3DenseDecodeOp, Qwen3PrefillOp, _hip  # noqa: E402
 
