@@ -7,7 +7,8 @@
 //
 // Block tile 256 x 256, K-steps of 64; 8 waves (2 per SIMD), wave (g, wn)
 // owning rows 128 g .. +127 and columns 64 wn .. +63 of the tile: 4 x 2
-// v_mfma_f32_32x32x16_bf16 accumulators (128 fp32 per lane).  Operand layout
+// v_mfma_f32_32x32x16_bf16 accumulators (128 fp32 per lane).  GEMMs with
+// fewer tiles than half the CUs use 256 x 128 tiles (waves of 128 x 32).  Operand layout
 // of the 32x32x16 MFMA: lane 32h + i holds A[i][8h .. 8h+7] and
 // B[8h .. 8h+7][i]; reg r of lane 32h + j holds C[8(r/4) + 4h + r%4][j].  With
 // A = X rows and B[k][n] = W[n][k], both operands are 16-byte pieces of K-rows.
@@ -87,6 +88,23 @@ __device__ __forceinline__ void frag_issue(const uint32_t (&addr)[6], u32x4v_t* 
       : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5])
       : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]), "v"(addr[5]));
 }
+// The same for 128-column tiles: 4 A pieces and 1 B piece per substep.
+__device__ __forceinline__ void frag_issue(const uint32_t (&addr)[5], u32x4v_t* r) {
+  asm volatile(
+      "ds_read_b128 %0, %5\n\t"
+      "ds_read_b128 %1, %6\n\t"
+      "ds_read_b128 %2, %7\n\t"
+      "ds_read_b128 %3, %8\n\t"
+      "ds_read_b128 %4, %9"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4])
+      : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]));
+}
+__device__ __forceinline__ void frag_wait(u32x4v_t (&f)[20]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]), "+v"(f[7]),
+                 "+v"(f[8]), "+v"(f[9]), "+v"(f[10]), "+v"(f[11]), "+v"(f[12]), "+v"(f[13]), "+v"(f[14]),
+                 "+v"(f[15]), "+v"(f[16]), "+v"(f[17]), "+v"(f[18]), "+v"(f[19]));
+}
 __device__ __forceinline__ void frag_wait(u32x4v_t (&f)[24]) {
   asm volatile("s_waitcnt lgkmcnt(0)"
                : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]), "+v"(f[7]),
@@ -100,14 +118,21 @@ __device__ __forceinline__ void frag_wait(u32x4v_t (&f)[24]) {
 // epilogue writes silu(gate) * up for those 128 features: the prefill's
 // SwiGLU without the [M, 2 IS] intermediate.  Rounding as the separate pass:
 // gate and up rounded to bf16, the activation rounded, the product rounded.
-template <bool SWIGLU>
+// NB: 32-column blocks per wave, 2 for 256-column tiles, 1 for 128-column
+// tiles (the same schedule and the same per-element accumulation order over
+// K, so both widths give bit-identical results; narrow tiles put twice the
+// blocks on the CUs when wide ones would leave most of them idle).
+template <bool SWIGLU, int NB>
 __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) void gemm_bf16_kernel(GemmArgs a) {
+  static_assert(NB == 2 || (NB == 1 && !SWIGLU), "tile widths 256 and 128 (SwiGLU: 256)");
+  constexpr int BN = 128 * NB, WC = 32 * NB;     // tile columns, columns per wave
+  constexpr int kDmaW = kGDma * NB / 2;         // W loads per thread of group 1 and K-step
   EZ_PROF_WAVE(kProfGemm);
   // Two stages of X and W tiles; after the K loop the same 128 KiB holds the
   // block's C tile in bf16 (16 KiB per wave) for row-contiguous stores.
-  __shared__ __align__(16) uint16_t lds[2 * (kGM + kGN) * kGK];
+  __shared__ __align__(16) uint16_t lds[2 * (kGM + BN) * kGK];
   uint16_t(*As)[kGM * kGK] = reinterpret_cast<uint16_t(*)[kGM * kGK]>(&lds[0]);
-  uint16_t(*Bs)[kGN * kGK] = reinterpret_cast<uint16_t(*)[kGN * kGK]>(&lds[2 * kGM * kGK]);
+  uint16_t(*Bs)[BN * kGK] = reinterpret_cast<uint16_t(*)[BN * kGK]>(&lds[2 * kGM * kGK]);
 
   // tile of this block: XCD-contiguous ranges, groups of kGroupM M-tiles
   const int ntiles = a.tm * a.tn;
@@ -115,7 +140,7 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) 
   if (ntiles % 8 == 0) t = (t % 8) * (ntiles / 8) + t / 8;
   const int grp = t / (kGroupM * a.tn), gi = t % (kGroupM * a.tn);
   const int gm = a.tm - grp * kGroupM < kGroupM ? a.tm - grp * kGroupM : kGroupM;
-  const int64_t m0 = int64_t(grp * kGroupM + gi % gm) * kGM, n0 = int64_t(gi / gm) * (SWIGLU ? kGN / 2 : kGN);
+  const int64_t m0 = int64_t(grp * kGroupM + gi % gm) * kGM, n0 = int64_t(gi / gm) * (SWIGLU ? kGN / 2 : BN);
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar LDS destinations
@@ -128,7 +153,7 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) 
   // depend on c (32 c rows go in the scalar offset).
   const int dr = 8 * wg + (lane >> 3), lc = (lane & 7) ^ ((dr >> 1) & 7);
   const uint32_t aoff = uint32_t((dr * a.ldx + lc * 8) * 2), boff = uint32_t((dr * a.K + lc * 8) * 2);
-  const int64_t mrows = a.M - m0 < kGM ? a.M - m0 : kGM, nrows = a.N - n0 < kGN ? a.N - n0 : kGN;
+  const int64_t mrows = a.M - m0 < kGM ? a.M - m0 : kGM, nrows = a.N - n0 < BN ? a.N - n0 : BN;
   const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(a.X + m0 * a.ldx), 0, int(((mrows - 1) * a.ldx + a.K) * 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
@@ -144,7 +169,7 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) 
   };
   auto dma_w = [&](int64_t k0, int buf) {
 #pragma unroll
-    for (int c = 0; c < kGDma; ++c) {
+    for (int c = 0; c < kDmaW; ++c) {
       const bool up = SWIGLU && c >= kGDma / 2;
       const int cr = up ? c - kGDma / 2 : c;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(up ? ures : wres,
@@ -155,11 +180,11 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) 
 
   // Fragment addresses (bytes within a tile): A row 128 g + 32 ra + i, B row
   // 64 wn + 32 rb + i; substep s reads logical chunk 2s + h.
-  uint32_t arow[4], brow[2];
+  uint32_t arow[4], brow[NB];
 #pragma unroll
   for (int ra = 0; ra < 4; ++ra) arow[ra] = uint32_t(128 * g + 32 * ra + i);
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) brow[rb] = uint32_t(64 * wn + 32 * rb + i);
+  for (int rb = 0; rb < NB; ++rb) brow[rb] = uint32_t(WC * wn + 32 * rb + i);
   const uint32_t abase[2] = {
       uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint16_t*)(&As[0][0]))),
       uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint16_t*)(&As[1][0])))};
@@ -167,26 +192,27 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) 
       uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint16_t*)(&Bs[0][0]))),
       uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint16_t*)(&Bs[1][0])))};
 
-  f32x16_t acc[4][2];
+  f32x16_t acc[4][NB];
 #pragma unroll
   for (int ra = 0; ra < 4; ++ra)
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int rb = 0; rb < NB; ++rb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[ra][rb][r] = 0.f;
 
-  u32x4v_t fr[24];  // one K-step: fr[6 s + ra] A pieces, fr[6 s + 4 + rb] B pieces
+  constexpr int FS = 4 + NB;  // fragments per substep
+  u32x4v_t fr[4 * FS];        // one K-step: fr[FS s + ra] A pieces, fr[FS s + 4 + rb] B pieces
   auto read_step = [&](int buf) {
 #pragma unroll
     for (int s = 0; s < kGK / 16; ++s) {
-      uint32_t addr[6];
+      uint32_t addr[FS];
 #pragma unroll
       for (int ra = 0; ra < 4; ++ra)
         addr[ra] = abase[buf] + arow[ra] * kGRowBytes + (((2 * s + h) ^ ((arow[ra] >> 1) & 7)) << 4);
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
+      for (int rb = 0; rb < NB; ++rb)
         addr[4 + rb] = bbase[buf] + brow[rb] * kGRowBytes + (((2 * s + h) ^ ((brow[rb] >> 1) & 7)) << 4);
-      frag_issue(addr, &fr[6 * s]);
+      frag_issue(addr, &fr[FS * s]);
     }
     frag_wait(fr);
   };
@@ -196,9 +222,9 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) 
 #pragma unroll
       for (int ra = 0; ra < 4; ++ra)
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-          acc[ra][rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, fr[6 * s + ra]),
-                                                                __builtin_bit_cast(bf16x8_t, fr[6 * s + 4 + rb]),
+        for (int rb = 0; rb < NB; ++rb)
+          acc[ra][rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, fr[FS * s + ra]),
+                                                                __builtin_bit_cast(bf16x8_t, fr[FS * s + 4 + rb]),
                                                                 acc[ra][rb], 0, 0, 0);
   };
   auto barrier = [&]() {
@@ -226,7 +252,7 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) 
     } else if (j + 2 < nk) {
       dma_w((j + 2) * kGK, buf);
       __builtin_amdgcn_sched_barrier(0);
-      wait_vm<kGDma>();  // W of step j + 1 (the older loads)
+      wait_vm<kDmaW>();  // W of step j + 1 (the older loads)
     } else {
       __builtin_amdgcn_sched_barrier(0);
       wait_vm<0>();
@@ -242,18 +268,19 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) 
   if (g == 0) barrier();  // the same barrier count for both groups
 
   // Epilogue.  Reg r of lane (h, i) in acc[ra][rb] is C[32 ra + 8(r/4) + 4h +
-  // r%4][32 rb + i] of the wave's 128 x 64 tile: rounded to bf16 into the
-  // wave's LDS slot (row-major, 128 bytes a row), then read back 16 bytes a
-  // lane (8 rows per instruction) for 16-byte stores and residual loads.
+  // r%4][32 rb + i] of the wave's 128 x WC tile: rounded to bf16 into the
+  // wave's LDS slot (row-major, 2 WC bytes a row), then read back 16 bytes a
+  // lane (64 / (WC / 8) rows per instruction) for 16-byte stores and residual
+  // loads.
   __syncthreads();  // every wave is done with the operand tiles
-  uint16_t* ct = &lds[wave * 128 * 64];
+  uint16_t* ct = &lds[wave * 128 * WC];
 #pragma unroll
   for (int ra = 0; ra < 4; ++ra)
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int rb = 0; rb < NB; ++rb)
 #pragma unroll
       for (int r = 0; r < 16; ++r)
-        ct[(32 * ra + 8 * (r >> 2) + 4 * h + (r & 3)) * 64 + 32 * rb + i] = f2bf(acc[ra][rb][r]);
+        ct[(32 * ra + 8 * (r >> 2) + 4 * h + (r & 3)) * WC + 32 * rb + i] = f2bf(acc[ra][rb][r]);
   if constexpr (SWIGLU) {
     // Wave (g, wn) of the group finalises rows 128 g + 32 wn .. +31 of the
     // 128 features; gate column c of the tile lives in wave (g, c / 64), up
@@ -283,13 +310,14 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) 
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's writes are in LDS before its reads
   const bool vec = a.ldy % 8 == 0 && (reinterpret_cast<uintptr_t>(a.Y) & 15) == 0 &&
                    (!a.R || (reinterpret_cast<uintptr_t>(a.R) & 15) == 0);
-  const int lr = lane >> 3, lcb = (lane & 7) * 8;
+  constexpr int LPR = WC / 8, RPI = kWave / LPR;  // lanes per row, rows per instruction
+  const int lr = lane / LPR, lcb = (lane % LPR) * 8;
 #pragma unroll 4
-  for (int q = 0; q < 16; ++q) {
-    const int rr = 8 * q + lr;
-    const int64_t row = m0 + 128 * g + rr, col = n0 + 64 * wn + lcb;
+  for (int q = 0; q < 128 / RPI; ++q) {
+    const int rr = RPI * q + lr;
+    const int64_t row = m0 + 128 * g + rr, col = n0 + WC * wn + lcb;
     if (row >= a.M || col >= a.N) continue;
-    const uint4 cv = *reinterpret_cast<const uint4*>(&ct[rr * 64 + lcb]);
+    const uint4 cv = *reinterpret_cast<const uint4*>(&ct[rr * WC + lcb]);
     uint16_t* y = a.Y + row * a.ldy + col;
     if (vec && col + 8 <= a.N) {
       uint4 out = cv;
@@ -330,8 +358,19 @@ bool gemm_mfma_supported(const uint16_t* X, int64_t ldx, const uint16_t* W, cons
 int gemm_mfma(const uint16_t* X, int64_t ldx, const uint16_t* W, uint16_t* Y, int64_t ldy, const uint16_t* R,
               int64_t M, int64_t N, int64_t K, hipStream_t s) {
   EZ_REQUIRE(gemm_mfma_supported(X, ldx, W, Y, ldy, R, M, N, K), "gemm: shape or alignment not supported by the MFMA kernel");
-  GemmArgs a{X, ldx, W, Y, ldy, R, M, N, K, int((M + kGM - 1) / kGM), int((N + kGN - 1) / kGN), 0};
-  hipLaunchKernelGGL(gemm_bf16_kernel<false>, dim3(unsigned(a.tm * a.tn)), dim3(kGThreads), 0, s, a);
+  // Fewer 256-wide tiles than half the CUs (short prompts): 128-wide tiles,
+  // twice the blocks (o_proj at T = 1024: 85 -> 70 us; same results).  A
+  // part-filled last round of a longer GEMM gains nothing from narrow tiles
+  // (QKV at T = 4096: 180 us either way): a narrow tile takes nearly as long
+  // as a wide one, its X stream and fragment reads being the same.
+  const int64_t tm = (M + kGM - 1) / kGM, tn = (N + kGN - 1) / kGN, cus = num_cus();
+  if (2 * tm * tn <= cus) {
+    GemmArgs a{X, ldx, W, Y, ldy, R, M, N, K, int(tm), int((N + 127) / 128), 0};
+    hipLaunchKernelGGL((gemm_bf16_kernel<false, 1>), dim3(unsigned(a.tm * a.tn)), dim3(kGThreads), 0, s, a);
+  } else {
+    GemmArgs a{X, ldx, W, Y, ldy, R, M, N, K, int(tm), int(tn), 0};
+    hipLaunchKernelGGL((gemm_bf16_kernel<false, 2>), dim3(unsigned(a.tm * a.tn)), dim3(kGThreads), 0, s, a);
+  }
   return launch_status("gemm (MFMA)");
 }
 
@@ -347,7 +386,7 @@ int gemm_swiglu(const uint16_t* X, int64_t ldx, const uint16_t* W, uint16_t* Y, 
   EZ_REQUIRE(gemm_swiglu_supported(X, ldx, W, Y, ldy, M, IS, K),
              "gemm_swiglu: shape or alignment not supported (IS % 128, K % 64, 16-byte rows)");
   GemmArgs a{X, ldx, W, Y, ldy, nullptr, M, 2 * IS, K, int((M + kGM - 1) / kGM), int(IS / (kGN / 2)), IS};
-  hipLaunchKernelGGL(gemm_bf16_kernel<true>, dim3(unsigned(a.tm * a.tn)), dim3(kGThreads), 0, s, a);
+  hipLaunchKernelGGL((gemm_bf16_kernel<true, 2>), dim3(unsigned(a.tm * a.tn)), dim3(kGThreads), 0, s, a);
   return launch_status("gemm_swiglu (MFMA)");
 }
 

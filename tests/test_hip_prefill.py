@@ -115,6 +115,25 @@ def test_gemm_vs_oracle(M, N, K, resid):
         assert torch.equal(Y, Y2)
 
 
+def test_gemm_tile_widths_bit_identical():
+    """256- and 128-column tiles accumulate every output over K in the same
+    order: the same rows computed in a launch of wide tiles (4096 x 4096:
+    256 tiles, one round) and of narrow tiles (2048 x 4096: 128 wide tiles
+    would fill half the CUs, so it runs 256 narrow ones) are bit-identical."""
+    torch.manual_seed(5)
+    K = N = 4096
+    X = torch.randn(4096, K, device="cuda").to(torch.bfloat16)
+    W = (torch.randn(N, K, device="cuda") * K ** -0.5).to(torch.bfloat16)
+    ws = torch.empty(_hip.size("ezops_gemm_workspace_size"), dtype=torch.uint8, device="cuda")
+    out = {}
+    for M in (4096, 2048):
+        Y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+        _hip.call("ezops_gemm_bf16", X.data_ptr(), K, W.data_ptr(), Y.data_ptr(), N, None, M, N, K, ws.data_ptr(),
+                  ws.numel(), _hip.stream())
+        out[M] = Y
+    assert torch.equal(out[4096][:2048], out[2048])
+
+
 @pytest.mark.parametrize("M,IS,K", [(300, 384, 256), (512, 1024, 512), (257, 128, 64)])
 def test_gemm_swiglu_vs_unfused(M, IS, K):
     """The fused gate/up + SwiGLU GEMM against the plain GEMM into [M, 2 IS]
