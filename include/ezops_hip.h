@@ -158,8 +158,8 @@ int ezops_paged_attn_decode_bf16(const void* Q, const void* K_pages, const void*
  * rows [0, past_lens[b] + i].  Cache K/V [B, Hkv, S, D], or page pools
  * [num_pages, Hkv, page_size, D] with block_table [B, S / page_size] when
  * block_table != NULL.  max_q_len: host bound on the per-sequence token
- * counts (grid size).  D = 128; H / Hkv in {1, 2, 4, 8}; scale <= 0 selects
- * 1/sqrt(D).  T: rows of Q / Out.  Offsets and lengths are clamped into
+ * counts (grid size).  D = 128; H / Hkv in {1, 2, 4, 8}; S < 2^23 (cache
+ * offsets are 32-bit); scale <= 0 selects 1/sqrt(D).  T: rows of Q / Out.  Offsets and lengths are clamped into
  * [0, T] rows and [0, S] cache rows on the device; rows at or beyond S are
  * skipped (left unwritten).
  * No counterpart in the reference (decode only, ezops/ops/attn_decode.py:9-67):
