@@ -66,6 +66,9 @@ def test_new_entry_points_reject_bad_arguments():
     # prefill attention: head_dim 128 only
     rc = lib.ezops_prefill_attn_bf16(d, d, d, d, d, None, 1, 16, 8, 8, 64, 64, 16, None, 0, 0, 0.0, None)
     assert rc == _hip.EINVAL and b"head_dim" in lib.ezops_hip_last_error()
+    # prefill attention: cache offsets are 32-bit, so S < 2^23 rows
+    rc = lib.ezops_prefill_attn_bf16(d, d, d, d, d, None, 1, 16, 8, 8, 1 << 23, 128, 16, None, 0, 0, 0.0, None)
+    assert rc == _hip.EINVAL and b"2^23" in lib.ezops_hip_last_error()
     # library GEMM: empty shapes
     assert lib.ezops_gemm_bf16(d, 16, d, d, 16, None, 0, 16, 16, d, 1 << 20, None) == _hip.EINVAL
     # layer prefill: cu_seqlens is required
