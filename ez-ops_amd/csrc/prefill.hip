@@ -61,14 +61,20 @@ __device__ __forceinline__ const uint16_t* cache_row(const PrefillAttnArgs& a, c
 
 typedef unsigned int u32x4v_t __attribute__((ext_vector_type(4)));
 
-// Reads 8 K fragments from LDS and waits for them.  One asm block without a
-// memory clobber: the compiler's own wait insertion treats any LDS read after
-// an LDS DMA as dependent on every outstanding load and would wait (vmcnt 0)
-// for the next tile's prefetch here; these reads touch the other buffer, and
-// the volatile asm keeps its place between the barriers that order them
-// against the DMA into that buffer.
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
+
+// LDS fragment reads as asm blocks without a memory clobber, issued apart
+// from their waits: the compiler's own wait insertion treats any LDS read
+// after an LDS DMA as dependent on every outstanding load and would wait
+// (vmcnt 0) for the next tile's prefetch; these reads touch the other
+// buffer, and the volatile asm keeps its place between the barriers that
+// order them against the DMA into that buffer.  A read group is issued one
+// step ahead of its use and waited for by lds_wait8 / lds_waitv, which take
+// the registers as operands so that no use is scheduled before the wait.
+//
+// lds_issue8: the 8 K fragments (k-steps) of 32 key rows.
 template <int OFF>
-__device__ __forceinline__ void lds_read8(const uint32_t (&addr)[8], u32x4v_t (&r)[8]) {
+__device__ __forceinline__ void lds_issue8(const uint32_t (&addr)[8], u32x4v_t (&r)[8]) {
   asm volatile(
       "ds_read_b128 %0, %8 offset:%16\n\t"
       "ds_read_b128 %1, %9 offset:%16\n\t"
@@ -77,22 +83,19 @@ __device__ __forceinline__ void lds_read8(const uint32_t (&addr)[8], u32x4v_t (&
       "ds_read_b128 %4, %12 offset:%16\n\t"
       "ds_read_b128 %5, %13 offset:%16\n\t"
       "ds_read_b128 %6, %14 offset:%16\n\t"
-      "ds_read_b128 %7, %15 offset:%16\n\t"
-      "s_waitcnt lgkmcnt(0)"
+      "ds_read_b128 %7, %15 offset:%16"
       : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
       : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]), "v"(addr[5]), "v"(addr[6]),
         "v"(addr[7]), "i"(OFF));
 }
-static_assert(kPD / 16 == 8, "lds_read8 reads the 8 k-steps of a 128-dim key row");
-typedef int i32x2_t __attribute__((ext_vector_type(2)));
-// The 4 V^T operands (dimension blocks d = 0..3) of one 16-key step by
-// transposing LDS reads (ds_read_b64_tr_b16: in each 16-lane group, lane m
-// receives element m%4 of the 8-byte rows that lanes m/4, 4 + m/4, 8 + m/4
-// and 12 + m/4 address): r[2d] from addr[d] + OFF, r[2d+1] 8 key rows
-// further.  One asm block with its own wait, for the same reason as
-// lds_read8.
+static_assert(kPD / 16 == 8, "lds_issue8 reads the 8 k-steps of a 128-dim key row");
+// lds_issue_vt4: the 4 V^T operands (dimension blocks d = 0..3) of one
+// 16-key step by transposing reads (ds_read_b64_tr_b16: in each 16-lane
+// group, lane m receives element m%4 of the 8-byte rows that lanes m/4,
+// 4 + m/4, 8 + m/4 and 12 + m/4 address): r[2d] from addr[d] + OFF,
+// r[2d+1] 8 key rows further.
 template <int OFF>
-__device__ __forceinline__ void lds_read_vt4(const uint32_t (&addr)[4], i32x2_t (&r)[8]) {
+__device__ __forceinline__ void lds_issue_vt4(const uint32_t (&addr)[4], i32x2_t (&r)[8]) {
   asm volatile(
       "ds_read_b64_tr_b16 %0, %8 offset:%12\n\t"
       "ds_read_b64_tr_b16 %1, %8 offset:%13\n\t"
@@ -101,12 +104,24 @@ __device__ __forceinline__ void lds_read_vt4(const uint32_t (&addr)[4], i32x2_t 
       "ds_read_b64_tr_b16 %4, %10 offset:%12\n\t"
       "ds_read_b64_tr_b16 %5, %10 offset:%13\n\t"
       "ds_read_b64_tr_b16 %6, %11 offset:%12\n\t"
-      "ds_read_b64_tr_b16 %7, %11 offset:%13\n\t"
-      "s_waitcnt lgkmcnt(0)"
+      "ds_read_b64_tr_b16 %7, %11 offset:%13"
       : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
       : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "i"(OFF), "i"(OFF + 8 * kPD * 2));
 }
-static_assert(kPD / 32 == 4, "lds_read_vt4 reads the 4 dimension blocks of a 128-dim head");
+static_assert(kPD / 32 == 4, "lds_issue_vt4 reads the 4 dimension blocks of a 128-dim head");
+// Waits until at most N LDS reads are outstanding (they complete in order).
+template <int N>
+__device__ __forceinline__ void lds_wait8(u32x4v_t (&r)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(%8)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7])
+               : "i"(N));
+}
+template <int N>
+__device__ __forceinline__ void lds_waitv(i32x2_t (&r)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(%8)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7])
+               : "i"(N));
+}
 
 // Block = (query tile, sequence, kv head, head group of HPB = min(G, 4) query
 // heads); wave w serves query head kvh*G + hb*HPB + w%HPB, query rows
@@ -259,17 +274,25 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
 
     if (k0 <= wave_last) {  // a wave whose queries all precede the tile skips it
       f32x16_t st[kBK / 32];
+      {
+        u32x4v_t kf0[kPD / 16], kf1[kPD / 16];
+        lds_issue8<BUF * kBufBytes>(kaddr, kf0);
+        lds_issue8<BUF * kBufBytes + 32 * kPD * 2>(kaddr, kf1);
 #pragma unroll
-      for (int kk = 0; kk < kBK / 32; ++kk) {
+        for (int kk = 0; kk < kBK / 32; ++kk)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) st[kk][r] = 0.f;
-        u32x4v_t kf[kPD / 16];
-        if (kk == 0) lds_read8<BUF * kBufBytes>(kaddr, kf);
-        else lds_read8<BUF * kBufBytes + 32 * kPD * 2>(kaddr, kf);
+          for (int r = 0; r < 16; ++r) st[kk][r] = 0.f;
+        lds_wait8<8>(kf0);
 #pragma unroll
         for (int s = 0; s < kPD / 16; ++s)
-          st[kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[s]), qf[s], st[kk], 0, 0, 0);
+          st[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf0[s]), qf[s], st[0], 0, 0, 0);
+        lds_wait8<0>(kf1);
+#pragma unroll
+        for (int s = 0; s < kPD / 16; ++s)
+          st[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf1[s]), qf[s], st[1], 0, 0, 0);
       }
+      i32x2_t vfa[2 * (kPD / 32)], vfb[2 * (kPD / 32)];
+      lds_issue_vt4<BUF * kBufBytes>(vaddr, vfa);  // V^T of the first 16-key step, under the softmax
       // st[kk][r] = S[query j][key k0 + 32kk + 8(r/4) + 4h + r%4] (unscaled)
       if (k0 + kBK - 1 > past + qi0) {  // diagonal tile: causal mask (32-bit offsets)
         const int lim = int(qpos - k0) - 4 * h;
@@ -315,11 +338,14 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
           }
           const bf16x8_t pb = as_bf16x8(make_uint4(w[0], w[1], w[2], w[3]));
           // keys 32kk + 16u + 4h + 0..3 and + 8..11 of dims 32d + j
-          i32x2_t vf[2 * (kPD / 32)];
-          if (kk == 0 && u == 0) lds_read_vt4<BUF * kBufBytes>(vaddr, vf);
-          else if (kk == 0) lds_read_vt4<BUF * kBufBytes + 16 * kPD * 2>(vaddr, vf);
-          else if (u == 0) lds_read_vt4<BUF * kBufBytes + 32 * kPD * 2>(vaddr, vf);
-          else lds_read_vt4<BUF * kBufBytes + 48 * kPD * 2>(vaddr, vf);
+          // the next step's V^T reads go out before this step's wait
+          const int t = 2 * kk + u;
+          if (t == 0) lds_issue_vt4<BUF * kBufBytes + 16 * kPD * 2>(vaddr, vfb);
+          else if (t == 1) lds_issue_vt4<BUF * kBufBytes + 32 * kPD * 2>(vaddr, vfa);
+          else if (t == 2) lds_issue_vt4<BUF * kBufBytes + 48 * kPD * 2>(vaddr, vfb);
+          i32x2_t(&vf)[2 * (kPD / 32)] = (t & 1) ? vfb : vfa;
+          if (t < 3) lds_waitv<8>(vf);
+          else lds_waitv<0>(vf);
 #pragma unroll
           for (int d = 0; d < kPD / 32; ++d) {
             const bf16x8_t va = __builtin_bit_cast(
