@@ -256,12 +256,13 @@ extern "C" int ezops_qwen3_decode_step_bf16(const ezops_qwen3_layer* layers, int
 
 // ---------------------------------------------------------------------------
 // Prefill of one Qwen3 dense layer: T new tokens (the sequences' chunks back
-// to back) through RMSNorm -> QKV GEMM -> q/k norm + RoPE + cache write ->
-// causal flash attention -> o_proj GEMM (+residual) -> RMSNorm -> gate/up
-// GEMM -> SwiGLU -> down GEMM (+residual).
+// to back) through RMSNorm -> QKV GEMM -> k norm + RoPE + cache write of k and
+// v -> causal flash attention (q norm + RoPE as it loads q from the QKV rows)
+// -> o_proj GEMM (+residual) -> RMSNorm -> gate/up GEMM -> SwiGLU -> down
+// GEMM (+residual).
 namespace {
 struct PrefillBufs {
-  uint16_t *xn, *qkv, *qn, *att, *h, *gu, *act;
+  uint16_t *xn, *qkv, *att, *h, *gu, *act;
   void* gemm_ws;
 };
 size_t prefill_ws(const ezops_qwen3_layer* p, int64_t T, PrefillBufs* b, char* base) {
@@ -271,7 +272,6 @@ size_t prefill_ws(const ezops_qwen3_layer* p, int64_t T, PrefillBufs* b, char* b
   PrefillBufs t{};
   t.xn = take(T * p->HS);
   t.qkv = take(T * QKV);
-  t.qn = take(T * QR);
   t.att = take(T * QR);
   t.h = take(T * p->HS);
   t.gu = take(T * 2 * p->IS);
@@ -318,7 +318,7 @@ extern "C" int ezops_qwen3_prefill_bf16(const ezops_qwen3_layer* p, int64_t T, c
   r.qw = W(p->q_norm_w); r.kw = W(p->k_norm_w);
   r.cos = W(p->cos); r.sin = W(p->sin);
   r.Kc = static_cast<uint16_t*>(p->K_cache); r.Vc = static_cast<uint16_t*>(p->V_cache);
-  r.q_out = w.qn;
+  r.q_out = nullptr;  // k / v only: the attention normalises and rotates q as it loads it
   r.B = T; r.H = p->H; r.Hkv = p->Hkv; r.D = p->D; r.S = p->S;
   r.cu = cu_seqlens; r.past = p->kv_lens; r.nseq = p->B;
   r.eps = p->eps;
@@ -330,7 +330,8 @@ extern "C" int ezops_qwen3_prefill_bf16(const ezops_qwen3_layer* p, int64_t T, c
   if (rc) return rc;
 
   PrefillAttnArgs a{};
-  a.Q = w.qn; a.q_rs = QR;
+  a.Q = w.qkv; a.q_rs = QKV;
+  a.q_raw = 1; a.qw = r.qw; a.qcos = r.cos; a.qsin = r.sin; a.qeps = p->eps;
   a.K = r.Kc; a.V = r.Vc;
   a.Out = w.att; a.o_rs = QR;
   a.cu = cu_seqlens; a.past = p->kv_lens;

@@ -58,7 +58,7 @@ struct QkRopeArgs {
   const uint16_t* qw; const uint16_t* kw;
   const uint16_t* cos; const uint16_t* sin;
   uint16_t* Kc; uint16_t* Vc;
-  uint16_t* q_out; uint16_t* k_out;
+  uint16_t* q_out; uint16_t* k_out;  // q_out NULL: the k / v heads only (q is left to its consumer)
   int64_t B, H, Hkv, D, S;
   int64_t position; const int32_t* positions; int64_t pos_offset;
   float eps;
@@ -108,6 +108,11 @@ struct PrefillAttnArgs {
   const int32_t* block_table; int64_t bt_stride; int page_size; int64_t num_pages;
   int64_t B, T, H, Hkv, S, D, max_q;  // T: rows of Q / Out
   float scale;
+  // Raw q (q_raw != 0, the layer's QKV rows): each query head gets the
+  // per-head RMSNorm (weight qw, NULL = unit; eps) and the half-split RoPE
+  // at its cache position (cos / sin rows, NULL = none) as it is loaded,
+  // rounded to bf16 as the separate QK-norm + RoPE stage rounds it.
+  int q_raw; const uint16_t* qw; const uint16_t* qcos; const uint16_t* qsin; float qeps;
 };
 int launch_prefill_attn(const PrefillAttnArgs& a, hipStream_t s);
 int launch_silu_mul(const uint16_t* gu, uint16_t* out, int64_t T, int64_t IS, hipStream_t s);

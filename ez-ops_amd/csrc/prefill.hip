@@ -166,8 +166,68 @@ __global__ __launch_bounds__(kPW * kWave) __attribute__((amdgpu_waves_per_eu(2))
   bf16x8_t qf[kPD / 16];
   {
     const uint16_t* qp = a.Q + (q0 + qrow) * a.q_rs + int64_t(hq) * kPD + 8 * h;
+    uint4 qr[kPD / 16];
 #pragma unroll
-    for (int s = 0; s < kPD / 16; ++s) qf[s] = as_bf16x8(*reinterpret_cast<const uint4*>(qp + 16 * s));
+    for (int s = 0; s < kPD / 16; ++s) qr[s] = *reinterpret_cast<const uint4*>(qp + 16 * s);
+    if (!a.q_raw) {
+#pragma unroll
+      for (int s = 0; s < kPD / 16; ++s) qf[s] = as_bf16x8(qr[s]);
+    } else {
+      // Fragment s of lane half h holds dims 16 s + 8 h .. +7: this lane has
+      // 64 of the head's dims, the other half the rest; RoPE partners (i,
+      // i + 64) are fragments s and s + 4 of the same lane.  The weight and
+      // cos / sin loads go out with the q loads, unconditionally (a missing
+      // table reads q's own row and its values are not used).
+      const int64_t crow = qpos * kPD + 8 * h;  // cos / sin row of the query's cache position
+      const uint16_t* wp = a.qw ? a.qw + 8 * h : qp;
+      const uint16_t* cp = a.qcos ? a.qcos + crow : qp;
+      const uint16_t* sp = a.qcos ? a.qsin + crow : qp;
+      uint4 wr[kPD / 16], cr[kPD / 16], sr[kPD / 16];
+#pragma unroll
+      for (int s = 0; s < kPD / 16; ++s) {
+        wr[s] = *reinterpret_cast<const uint4*>(wp + 16 * s);
+        cr[s] = *reinterpret_cast<const uint4*>(cp + 16 * s);
+        sr[s] = *reinterpret_cast<const uint4*>(sp + 16 * s);
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int s = 0; s < kPD / 16; ++s) {
+        float x[8];
+        unpack8(qr[s], x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+      }
+      const float r = rsqrtf(halves_sum(ss) / float(kPD) + a.qeps);
+      const bool use_w = a.qw != nullptr, rope = a.qcos != nullptr;
+#pragma unroll
+      for (int s = 0; s < kPD / 32; ++s) {
+        float y1[8], y2[8], w1[8], w2[8], c1[8], c2[8], s1[8], s2[8];
+        unpack8(qr[s], y1);
+        unpack8(qr[s + 4], y2);
+        unpack8(wr[s], w1);
+        unpack8(wr[s + 4], w2);
+        unpack8(cr[s], c1);
+        unpack8(cr[s + 4], c2);
+        unpack8(sr[s], s1);
+        unpack8(sr[s + 4], s2);
+        float o1[8], o2[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          y1[e] = __fmul_rn(y1[e], r);
+          y2[e] = __fmul_rn(y2[e], r);
+          if (use_w) {
+            y1[e] = __fmul_rn(y1[e], w1[e]);
+            y2[e] = __fmul_rn(y2[e], w2[e]);
+          }
+          o1[e] = rope ? __fadd_rn(__fmul_rn(y1[e], c1[e]), __fmul_rn(-y2[e], s1[e])) : y1[e];
+          o2[e] = rope ? __fadd_rn(__fmul_rn(y2[e], c2[e]), __fmul_rn(y1[e], s2[e])) : y2[e];
+        }
+        qf[s] = as_bf16x8(make_uint4(pack_bf2(o1[0], o1[1]), pack_bf2(o1[2], o1[3]), pack_bf2(o1[4], o1[5]),
+                                     pack_bf2(o1[6], o1[7])));
+        qf[s + 4] = as_bf16x8(make_uint4(pack_bf2(o2[0], o2[1]), pack_bf2(o2[2], o2[3]), pack_bf2(o2[4], o2[5]),
+                                         pack_bf2(o2[6], o2[7])));
+      }
+    }
   }
 
   f32x16_t o[kPD / 32];
@@ -418,6 +478,9 @@ int launch_prefill_attn(const PrefillAttnArgs& a, hipStream_t s) {
   EZ_REQUIRE(!a.block_table || (a.page_size >= 32 && (a.page_size & (a.page_size - 1)) == 0 &&
                                 a.S == a.bt_stride * a.page_size && a.num_pages >= 1),
              "prefill_attn: page_size must be a power of two >= 32 and S = max_pages * page_size");
+  EZ_REQUIRE(!a.q_raw || ((a.qcos == nullptr) == (a.qsin == nullptr) && (!a.qw || aligned16(a.qw)) &&
+                          (!a.qcos || (aligned16(a.qcos) && aligned16(a.qsin)))),
+             "prefill_attn: q norm weight and cos / sin tables must be 16-byte aligned, cos and sin together");
   if (a.max_q == 0) return 0;
   PrefillAttnArgs aa = a;
   if (aa.scale <= 0.f) aa.scale = 1.f / sqrtf(float(kPD));

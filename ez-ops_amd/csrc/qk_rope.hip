@@ -122,11 +122,12 @@ __global__ __launch_bounds__(256) void qk_norm_rope_vec_kernel(QkRopeArgs a) {
   constexpr int HPW = kWave / LPH;
   const int lane = threadIdx.x & (kWave - 1);
   const int l = lane % LPH;
-  const int64_t heads = a.H + a.Hkv;
+  const int64_t h0 = a.q_out ? 0 : a.H;  // without q_out, the kv heads only
+  const int64_t heads = a.H + a.Hkv - h0;
   const int64_t hid = (int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6)) * HPW + lane / LPH;
   const bool live = hid < a.B * heads;
   const int64_t hc = live ? hid : 0;  // dead lanes still join the exchanges, on a valid row
-  const int64_t b = hc / heads, h = hc % heads;
+  const int64_t b = hc / heads, h = h0 + hc % heads;
   const bool is_q = h < a.H;
   const int64_t kvh = h - a.H;
   int64_t seq, pos;
@@ -183,7 +184,7 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 }  // namespace
 
 int launch_qk_norm_rope(const QkRopeArgs& a, hipStream_t s) {
-  EZ_REQUIRE(a.q && a.k && a.v && a.Kc && a.Vc && a.q_out, "qk_norm_rope: null pointer");
+  EZ_REQUIRE(a.q && a.k && a.v && a.Kc && a.Vc, "qk_norm_rope: null pointer");
   EZ_REQUIRE(a.B >= 1 && a.H >= 1 && a.Hkv >= 1 && a.S >= 1, "qk_norm_rope: bad shape");
   EZ_REQUIRE(a.D >= 2 && a.D <= 2 * kMaxPairsPerLane * kWave && a.D % 2 == 0,
              "qk_norm_rope: head_dim must be even and <= %d", 2 * kMaxPairsPerLane * kWave);
@@ -192,10 +193,10 @@ int launch_qk_norm_rope(const QkRopeArgs& a, hipStream_t s) {
   EZ_REQUIRE(!a.block_table || (a.page_size >= 1 && (a.page_size & (a.page_size - 1)) == 0 && a.num_pages >= 1 &&
                                 a.S == a.bt_stride * a.page_size),
              "qk_norm_rope: paged cache needs a power-of-two page_size and S = max_pages * page_size");
-  const int64_t heads = a.B * (a.H + a.Hkv);
+  const int64_t heads = a.B * (a.q_out ? a.H + a.Hkv : a.Hkv);
   const bool vec = (a.D == 64 || a.D == 128 || a.D == 256) && a.q_bs % 8 == 0 && a.k_bs % 8 == 0 &&
                    a.v_bs % 8 == 0 && aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.Kc) &&
-                   aligned16(a.Vc) && aligned16(a.q_out) && (!a.k_out || aligned16(a.k_out)) &&
+                   aligned16(a.Vc) && (!a.q_out || aligned16(a.q_out)) && (!a.k_out || aligned16(a.k_out)) &&
                    (!a.qw || aligned16(a.qw)) && (!a.kw || aligned16(a.kw)) && (!a.cos || aligned16(a.cos)) &&
                    (!a.sin || aligned16(a.sin));
   if (vec) {
@@ -205,6 +206,7 @@ int launch_qk_norm_rope(const QkRopeArgs& a, hipStream_t s) {
     else if (a.D == 128) hipLaunchKernelGGL(qk_norm_rope_vec_kernel<128>, dim3(blocks), dim3(256), 0, s, a);
     else hipLaunchKernelGGL(qk_norm_rope_vec_kernel<256>, dim3(blocks), dim3(256), 0, s, a);
   } else {
+    EZ_REQUIRE(a.q_out, "qk_norm_rope: the k / v-only form needs head_dim 64, 128 or 256 and 16-byte rows");
     hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(unsigned((heads + 3) / 4)), dim3(256), 0, s, a);
   }
   return launch_status("qk_norm_rope");
@@ -230,6 +232,7 @@ extern "C" int ezops_qk_norm_rope_bf16(const void* q, int64_t q_bs, const void* 
   a.B = B; a.H = H; a.Hkv = Hkv; a.D = D; a.S = S;
   a.position = position; a.positions = positions; a.pos_offset = pos_offset;
   a.eps = eps;
+  EZ_REQUIRE(q_out, "qk_norm_rope: null pointer");
   EZ_REQUIRE(H % Hkv == 0, "qk_norm_rope: num_heads must be divisible by num_kv_heads");
   EZ_REQUIRE(positions || (position + pos_offset >= 0 && position + pos_offset < S),
              "qk_norm_rope: position out of range");
