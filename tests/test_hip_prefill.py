@@ -195,6 +195,24 @@ def test_qwen3_prefill_vs_oracle(q_lens, past, S):
     np.testing.assert_allclose(n(data[2]), Vc, **BF_TOL)  # V rows are QKV GEMM outputs
 
 
+@pytest.mark.parametrize("norm_weights,rope_theta", [(False, None), (True, None), (False, 1e6)])
+def test_qwen3_prefill_without_weights_or_rope(norm_weights, rope_theta):
+    """Unit norm weights and / or no RoPE (the attention's q transform with
+    its weight or tables absent) against the package's torch ref path."""
+    q_lens, past, S = [200, 57], [0, 300], 512
+    torch.manual_seed(7)
+    kw = dict(q_lens=q_lens, past_lens=past, num_kv_heads=8, norm_weights=norm_weights, rope_theta=rope_theta,
+              **QWEN3_8B)
+    op = Qwen3PrefillOp(2, S, backend="hip", **kw)
+    ref_op = Qwen3PrefillOp(2, S, backend="ref", **kw)
+    data = op.gen_data()
+    ref_data = [x.clone() for x in data]
+    out = op(*data)
+    ref = ref_op(*ref_data)
+    assert op.check(out, ref), (out.float() - ref.float()).norm().item() / ref.float().norm().item()
+    np.testing.assert_allclose(n(data[1]), n(ref_data[1]), **BF_TOL)  # cache rows written alike
+
+
 def test_qwen3_prefill_paged_equals_contiguous_then_decode():
     """Paged prefill equals contiguous prefill bit-for-bit (output and cache);
     the decode layer then continues from the prefilled cache."""
