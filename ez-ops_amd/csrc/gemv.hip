@@ -228,11 +228,17 @@ __device__ __forceinline__ void xfrag_fence(u32x4v_t (&x)[kMfmaSteps]) {
 // TPB > 1 (with CPW > 0): the block walks tiles blockIdx.x + k * gridDim.x,
 // k < TPB, as one stream of chunks, so the ring's DMAs for a tile's first
 // chunks are in flight during the previous tile's epilogue.
-template <int T, bool SILU, int CPW, int NW, int TPB>
+// R2 > 0 (T = 2, no SwiGLU): the block owns 16 + R2 consecutive rows, the
+// second MFMA tile holding rows 16 .. 16 + R2 - 1 (its other rows are never
+// loaded and their outputs never stored); both tiles share each X fragment,
+// so a block reads X once for 16 + R2 rows.
+template <int T, bool SILU, int CPW, int NW, int TPB, int R2 = 0>
 __global__ __launch_bounds__(NW * kWave) void linear_mfma_kernel(LinearArgs a) {
+  static_assert(R2 == 0 || (T == 2 && !SILU && TPB == 1 && R2 % 2 == 0 && R2 <= 16), "R2: two row tiles");
+  constexpr int kRowsPerBlock = R2 ? 16 + R2 : 16;
   EZ_PROF_WAVE(kProfLinearMfma);
   constexpr int XN = kMfmaSteps;         // X loads per chunk
-  constexpr int DN = T * kMfmaSlices;    // DMA slices per chunk
+  constexpr int DN = R2 ? kMfmaSlices + R2 / 2 : T * kMfmaSlices;  // DMA slices per chunk
   // One array per ring stage: distinct LDS objects.
   __shared__ __align__(16) uint4 Wl0[NW][T][kMfmaSlices][kWave];
   __shared__ __align__(16) uint4 Wl1[NW][T][kMfmaSlices][kWave];
@@ -242,7 +248,7 @@ __global__ __launch_bounds__(NW * kWave) void linear_mfma_kernel(LinearArgs a) {
   const int i = lane & 15, g = lane >> 4;
   const int64_t m0 = int64_t(blockIdx.y) * 16;
   const int64_t m = m0 + i;
-  int64_t row0 = int64_t(blockIdx.x) * 16;
+  int64_t row0 = int64_t(blockIdx.x) * kRowsPerBlock;
 
   // DMA lane roles: slice q of a chunk holds rows 2q, 2q+1 (lanes 0-31, 32-63);
   // lane piece cs = lane & 31 stores the row's 16-byte piece cs ^ r.
@@ -256,8 +262,14 @@ __global__ __launch_bounds__(NW * kWave) void linear_mfma_kernel(LinearArgs a) {
     const int64_t rows = a.N - r0 < 16 ? a.N - r0 : 16;
     wres0 = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.W + r0 * a.K), 0, int(rows * a.K * 2),
                                               0x00020000);
-    wres1 = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>((SILU ? a.W2 : a.W) + r0 * a.K), 0,
-                                              int(rows * a.K * 2), 0x00020000);
+    if constexpr (R2 > 0) {  // rows r0 + 16 .. r0 + 16 + R2 - 1 (past N: none, reads return zeros)
+      const int64_t rows1 = a.N - r0 - 16 < R2 ? (a.N - r0 - 16 > 0 ? a.N - r0 - 16 : 0) : R2;
+      wres1 = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.W + (rows1 ? r0 + 16 : 0) * a.K), 0,
+                                                int(rows1 * a.K * 2), 0x00020000);
+    } else {
+      wres1 = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>((SILU ? a.W2 : a.W) + r0 * a.K), 0,
+                                                int(rows * a.K * 2), 0x00020000);
+    }
 #pragma unroll
     for (int q = 0; q < kMfmaSlices; ++q) {
       int64_t row = 2 * q + dr;
@@ -277,9 +289,9 @@ __global__ __launch_bounds__(NW * kWave) void linear_mfma_kernel(LinearArgs a) {
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
-      for (int q = 0; q < kMfmaSlices; ++q)
+      for (int q = 0; q < (R2 && t ? R2 / 2 : kMfmaSlices); ++q)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(t ? wres1 : wres0, (__attribute__((address_space(3))) void*)(&stage[t][q][0]),
-                                                 16, woff[q], k0b, 0, 0);
+                                                 16, woff[q], k0b, 0, 2);
   };
   // Unconditional loads from clamped addresses: no branch around a pending load.
   // Packed X: the fragment of (batch block, k-step) is 1 KiB at a fixed place.
@@ -355,7 +367,12 @@ __global__ __launch_bounds__(NW * kWave) void linear_mfma_kernel(LinearArgs a) {
           for (int w = 0; w < NW; ++w) sacc += red[w][t][j][l];
           v[t] = sacc;
         }
-        store_out(a, mo, n, v[0], SILU ? v[1] : 0.f);
+        if constexpr (R2 > 0) {
+          store_out(a, mo, n, v[0], 0.f);
+          if (4 * (l >> 4) + j < R2 && n + 16 < a.N) store_out(a, mo, n + 16, v[1], 0.f);
+        } else {
+          store_out(a, mo, n, v[0], SILU ? v[1] : 0.f);
+        }
       }
     }
   };
@@ -643,6 +660,10 @@ void launch_valu_m(const LinearArgs& a, hipStream_t s) {
   }
 }
 
+#ifndef EZ_MFMA_R2
+#define EZ_MFMA_R2 1
+#endif
+
 template <bool SILU, int NW, int TPB = 1>
 void launch_mfma_nw(const LinearArgs& a, hipStream_t s) {
   constexpr int T = SILU ? 2 : 1;
@@ -655,6 +676,20 @@ void launch_mfma_nw(const LinearArgs& a, hipStream_t s) {
     case 2: EZ_MFMA_LAUNCH(2); break;
     case 4: EZ_MFMA_LAUNCH(4); break;
     case 6: EZ_MFMA_LAUNCH(6); break;
+    default: EZ_MFMA_LAUNCH(0); break;
+  }
+#undef EZ_MFMA_LAUNCH
+}
+
+// One block of 16 + R2 rows per CU (M <= 16), the two MFMA tiles sharing X.
+template <int R2>
+void launch_mfma_r2(const LinearArgs& a, hipStream_t s) {
+  const dim3 grid(unsigned((a.N + 15 + R2) / (16 + R2))), block(4 * kWave);
+  const int64_t nchunks = (a.K + kMfmaKC - 1) / kMfmaKC;
+  const int64_t cpw = nchunks % 4 == 0 ? nchunks / 4 : 0;
+#define EZ_MFMA_LAUNCH(C) hipLaunchKernelGGL((linear_mfma_kernel<2, false, C, 4, 1, R2>), grid, block, 0, s, a)
+  switch (cpw) {
+    case 4: EZ_MFMA_LAUNCH(4); break;
     default: EZ_MFMA_LAUNCH(0); break;
   }
 #undef EZ_MFMA_LAUNCH
@@ -680,7 +715,10 @@ void launch_mfma(const LinearArgs& a, hipStream_t s) {
     launch_mfma_nw<true, 4>(a, s);
   } else {
     const int64_t tiles = ((a.N + 15) / 16) * ((a.M + 15) / 16), cus = num_cus();
-    if (tiles > cus && tiles <= 2 * cus) launch_mfma_nw<false, 4>(a, s);
+    // 16 < rows per CU <= 24 (QKV of the model: 6144 rows, 24 per CU): one
+    // 24-row block per CU instead of 16-row tiles two to some CUs.
+    if (EZ_MFMA_R2 && a.M <= 16 && a.N > 16 * cus && a.N <= 24 * cus) launch_mfma_r2<8>(a, s);
+    else if (tiles > cus && tiles <= 2 * cus) launch_mfma_nw<false, 4>(a, s);
     else launch_mfma_nw<false, 8>(a, s);
   }
 }

@@ -375,3 +375,32 @@ def test_linear_stage_swiglu_multi_tile(M, N):
     np.testing.assert_allclose(n(Y), ref, rtol=2e-2, atol=3e-2)
     # N - 16 rows: not a multiple of the CU count, so one tile per block
     assert torch.equal(Y[:, : N - 16], run(N - 16))
+
+
+@pytest.mark.parametrize("M", [5, 16, 20])
+@pytest.mark.parametrize("extra,K", [(2048, 4096), (2048, 1032), (904, 4096), (8, 512)])
+@pytest.mark.parametrize("epi", [0, 1, 3])
+def test_linear_stage_24_row_blocks(M, extra, K, epi):
+    """M <= 16 with 16 < N / CUs <= 24 (QKV at B=16: 6144 rows over 256
+    CUs) runs one block of 16 + 8 rows per CU, the two MFMA tiles sharing
+    each X fragment; N = 16 * CUs + extra covers the full case (extra =
+    8 * CUs), a partial last block and a block whose second tile is empty.
+    M = 20 takes the 16-row tiles (two batch blocks) for comparison."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    N = 16 * cus + (extra if extra < 2048 else 8 * cus)
+    rng = np.random.default_rng(M + N + K + epi)
+    X = oracle.bf16(rng.standard_normal((M, K)).astype(np.float32))
+    W = oracle.bf16(rng.standard_normal((N, K)).astype(np.float32) * K ** -0.5)
+    R = oracle.bf16(rng.standard_normal((M, N)).astype(np.float32))
+    g_ = oracle.linear_bf16(X, W)
+    ref = {0: g_, 1: oracle.bf16(R + g_), 3: X @ W.T}[epi]
+    tX, tW, tR = g(X), g(W), g(R)
+    Y = torch.full((M, N), float("nan"), dtype=torch.float32 if epi == 3 else torch.bfloat16, device=DEV)
+    ws = torch.zeros(256, dtype=torch.uint8, device=DEV)
+    _hip.call("ezops_linear_stage_bf16", tX.data_ptr(), K, tW.data_ptr(), None, Y.data_ptr(), N,
+              tR.data_ptr(), N, None, 0, 1e-6, epi, M, N, K, ws.data_ptr(), ws.numel(), _hip.stream())
+    torch.cuda.synchronize()
+    if epi == 3:
+        np.testing.assert_allclose(n(Y), ref, rtol=1e-3, atol=1e-3)
+    else:
+        np.testing.assert_allclose(n(Y), ref, **BF_TOL)
