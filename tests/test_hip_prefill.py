@@ -134,6 +134,49 @@ def test_gemm_tile_widths_bit_identical():
     assert torch.equal(out[4096][:2048], out[2048])
 
 
+@pytest.mark.parametrize("M,N,K,res", [(4096, 6144, 4096, False), (4096, 4096, 4096, True), (4000, 6000, 4032, True),
+                                        (3000, 4100, 1088, False)])
+def test_gemm_full_and_partial_grid_bit_identical(M, N, K, res):
+    """A GEMM filling every CU and a 256-row launch of the same rows (narrow
+    tiles) agree bit for bit (each output accumulates over K in the same
+    order), with partial last tiles in M and N included; the whole output is
+    within the bf16 bar of torch's fp32 product."""
+    torch.manual_seed(M + N + K)
+    X = torch.randn(M, K, device="cuda").to(torch.bfloat16)
+    W = (torch.randn(N, K, device="cuda") * K ** -0.5).to(torch.bfloat16)
+    R = torch.randn(M, N, device="cuda").to(torch.bfloat16) if res else None
+    ws = torch.empty(_hip.size("ezops_gemm_workspace_size"), dtype=torch.uint8, device="cuda")
+    out = {}
+    for m in (M, 256):
+        Y = torch.empty(m, N, dtype=torch.bfloat16, device="cuda")
+        _hip.call("ezops_gemm_bf16", X.data_ptr(), K, W.data_ptr(), Y.data_ptr(), N,
+                  None if R is None else R.data_ptr(), m, N, K, ws.data_ptr(), ws.numel(), _hip.stream())
+        out[m] = Y
+    assert torch.equal(out[M][:256], out[256])
+    ref = X.float() @ W.float().T + (R.float() if res else 0)
+    torch.testing.assert_close(out[M].float(), ref, rtol=1e-2, atol=2e-2)
+
+
+def test_gemm_swiglu_full_and_partial_grid_bit_identical():
+    """The fused gate/up + SwiGLU GEMM over 4096 rows (512 tiles) and over
+    their first 256 rows (32 tiles) agree bit for bit on those rows, and
+    match torch's fp32 gate/up with SwiGLU."""
+    torch.manual_seed(9)
+    M, IS, K = 4096, 4096, 4096
+    X = torch.randn(M, K, device="cuda").to(torch.bfloat16)
+    W = (torch.randn(2 * IS, K, device="cuda") * K ** -0.5).to(torch.bfloat16)
+    out = {}
+    for m in (M, 256):
+        Y = torch.empty(m, IS, dtype=torch.bfloat16, device="cuda")
+        _hip.call("ezops_gemm_swiglu_bf16", X.data_ptr(), K, W.data_ptr(), Y.data_ptr(), IS, m, IS, K, _hip.stream())
+        out[m] = Y
+    assert torch.equal(out[M][:256], out[256])
+    gu = X[:512].float() @ W.float().T
+    g, u = gu[:, :IS], gu[:, IS:]
+    ref = torch.nn.functional.silu(g) * u
+    torch.testing.assert_close(out[M][:512].float(), ref, rtol=2e-2, atol=2e-2)
+
+
 @pytest.mark.parametrize("M,IS,K", [(300, 384, 256), (512, 1024, 512), (257, 128, 64)])
 def test_gemm_swiglu_vs_unfused(M, IS, K):
     """The fused gate/up + SwiGLU GEMM against the plain GEMM into [M, 2 IS]
