@@ -621,13 +621,15 @@ template <int M, int CH, bool NORM, bool SILU>
 void launch_rows(const LinearArgs& a, hipStream_t s) {
   constexpr int RB0 = CH <= 2 ? EZ_ROWS_RB4K : EZ_ROWS_RB12K;
   constexpr int RB = SILU ? (RB0 / 2 > 0 ? RB0 / 2 : 1) : RB0;
-  // Small matrices (<= 1024 blocks of RB rows): half the rows per block, so
-  // twice the blocks share the ramp (GEMV 4096 x 4096: 8.0 -> 7.8 us).
+  // Small matrices (<= 1024 blocks of RB rows): a quarter of the rows per
+  // block, so four times the blocks share the ramp (GEMV 4096 x 4096, RB 4 /
+  // 2 / 1: 8.0 / 7.7 / 7.5 us; one row per block everywhere made the
+  // layer's larger stages slower).
   if constexpr (RB > 2) {
     if ((a.N + RB - 1) / RB <= 1024) {
-      const int64_t blocks = (a.N + RB / 2 - 1) / (RB / 2);
-      hipLaunchKernelGGL((gemv_rows_kernel<M, RB / 2, CH, NORM, SILU>), dim3(unsigned(blocks)), dim3(kBlock), 0, s,
-                         a);
+      constexpr int RS = RB / 4 > 0 ? RB / 4 : 1;
+      const int64_t blocks = (a.N + RS - 1) / RS;
+      hipLaunchKernelGGL((gemv_rows_kernel<M, RS, CH, NORM, SILU>), dim3(unsigned(blocks)), dim3(kBlock), 0, s, a);
       return;
     }
   }
