@@ -623,8 +623,9 @@ void launch_rows(const LinearArgs& a, hipStream_t s) {
   constexpr int RB = SILU ? (RB0 / 2 > 0 ? RB0 / 2 : 1) : RB0;
   // Small matrices (<= 1024 blocks of RB rows): a quarter of the rows per
   // block, so four times the blocks share the ramp (GEMV 4096 x 4096, RB 4 /
-  // 2 / 1: 8.0 / 7.7 / 7.5 us; one row per block everywhere made the
-  // layer's larger stages slower).
+  // 2 / 1: 8.0 / 7.7 / 7.5 us).  Larger stages keep RB rows: the QKV
+  // projection (6144 rows, RMSNorm prologue, whose sum of squares every
+  // block computes) ran 10.5 / 11.1 / 12.0 us with 4 / 2 / 1 rows per block.
   if constexpr (RB > 2) {
     if ((a.N + RB - 1) / RB <= 1024) {
       constexpr int RS = RB / 4 > 0 ? RB / 4 : 1;
