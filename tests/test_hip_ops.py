@@ -320,10 +320,11 @@ def test_golden_qk_norm_rope_through_abi(golden):
 @pytest.mark.parametrize("M", [1, 3, 8, 16, 20])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3])
 @pytest.mark.parametrize("norm", [0, 1])
-@pytest.mark.parametrize("N,K", [(192, 512), (200, 1032)])
+@pytest.mark.parametrize("N,K", [(192, 512), (200, 1032), (200, 4096)])
 def test_linear_stage_epilogues(M, epi, norm, N, K):
-    """ezops_linear_stage_bf16: RMSNorm prologue x epilogues, VALU (M <= 4) and MFMA (M > 4) paths,
-    with partial weight tiles, partial K chunks and partial batch blocks."""
+    """ezops_linear_stage_bf16: RMSNorm prologue x epilogues, VALU (M <= 4; K = 4096 takes the
+    row-block kernel, one weight row per block at this N) and MFMA (M > 4) paths, with partial
+    weight tiles, partial K chunks and partial batch blocks."""
     rng = np.random.default_rng(100 * M + 10 * epi + norm + K)
     X = oracle.bf16(rng.standard_normal((M, K)).astype(np.float32))
     W = oracle.bf16(rng.standard_normal((N, K)).astype(np.float32) * K ** -0.5)
