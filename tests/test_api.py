@@ -230,3 +230,19 @@ def test_ref_prefill_layer_vs_oracle(paged):
     assert op.check(out, torch.from_numpy(ref))
     K1 = n(data[1]) if not paged else oracle.paged_to_contiguous(n(data[1]), bt, 32)
     np.testing.assert_allclose(K1, Kc, rtol=1e-2, atol=1e-2)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus N > 1 (or a WORLD_SIZE > 1 launch)
+    exits with status 2 and says why, before touching a device."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    for args, env in ((["--gpus", "2"], {}), ([], {"WORLD_SIZE": "2"})):
+        r = subprocess.run([sys.executable, str(root / "bench.py"), *args, "--steps", "1", "--warmup", "0"],
+                           capture_output=True, text=True, timeout=300, env={**os.environ, **env})
+        assert r.returncode == 2, (r.returncode, r.stdout[-500:], r.stderr[-500:])
+        assert "one GPU" in r.stdout + r.stderr
