@@ -376,6 +376,41 @@ __global__ __launch_bounds__(NW * kWave) void linear_mfma_kernel(LinearArgs a) {
       }
     }
   };
+  if constexpr (TPB < 0) {
+    // Streaming blocks: tiles row0, row0 + stride, ... below N (a run-time
+    // count), the two-stage ring running on from one tile's chunks into the
+    // next tile's, as in the multi-tile blocks.  CPW is even, so chunk cc
+    // always lives in stage cc & 1.
+    static_assert(CPW > 0 && CPW % 2 == 0 && R2 == 0, "streaming blocks need an even unrolled ring");
+    const int64_t stride = int64_t(gridDim.x) * 16;
+    dma(cb, Wl0[wave]);
+    xload(cb, xa);
+    dma(cb + 1, Wl1[wave]);
+    xload(cb + 1, xb);
+    for (int64_t r = row0; r < a.N; r += stride) {
+      const bool more = r + stride < a.N;
+#pragma unroll
+      for (int cc = 0; cc < CPW; ++cc) {
+        if (cc + 1 < CPW || more) wait_vm<DN + XN>(); else wait_vm<0>();
+        auto& x = (cc & 1) ? xb : xa;
+        auto* stage = (cc & 1) ? Wl1[wave] : Wl0[wave];
+        compute(cb + cc, stage, x);
+        if (cc + 2 < CPW) {
+          dma(cb + cc + 2, stage);
+          xload(cb + cc + 2, x);
+        } else if (more) {  // the next tile's first two chunks
+          if (cc + 2 == CPW) set_rows(r + stride);
+          dma(cb + cc + 2 - CPW, stage);
+          xload(cb + cc + 2 - CPW, x);
+        }
+      }
+      epilogue(r);
+#pragma unroll
+      for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      __syncthreads();  // red is rewritten by the next tile
+    }
+    return;
+  }
   if constexpr (TPB > 1) {
     static_assert(CPW > 0, "multi-tile blocks need the unrolled ring");
     constexpr int NC = TPB * CPW;
@@ -666,6 +701,9 @@ void launch_valu_m(const LinearArgs& a, hipStream_t s) {
 #ifndef EZ_MFMA_R2
 #define EZ_MFMA_R2 1
 #endif
+#ifndef EZ_MFMA_STREAM
+#define EZ_MFMA_STREAM 1
+#endif
 
 template <bool SILU, int NW, int TPB = 1>
 void launch_mfma_nw(const LinearArgs& a, hipStream_t s) {
@@ -698,6 +736,14 @@ void launch_mfma_r2(const LinearArgs& a, hipStream_t s) {
 #undef EZ_MFMA_LAUNCH
 }
 
+// Many 16-row tiles (at least 4 per CU: an LM head): two 4-wave streaming
+// blocks per CU, each walking its tiles with one DMA ring.
+void launch_mfma_stream(const LinearArgs& a, int64_t cus, hipStream_t s) {
+  const int64_t tn = (a.N + 15) / 16;
+  const dim3 grid(unsigned(tn < 2 * cus ? tn : 2 * cus), unsigned((a.M + 15) / 16)), block(4 * kWave);
+  hipLaunchKernelGGL((linear_mfma_kernel<1, false, 4, 4, -1>), grid, block, 0, s, a);
+}
+
 // Blocks of 16 weight rows (T=2: 16 gate + 16 up).  An 8-wave T=1 block
 // holds 136 KB of LDS, one per CU; when the tiles outnumber the CUs but not
 // twice over (QKV at 6144 rows: 384 tiles), 4-wave blocks (68 KB) share a CU
@@ -720,7 +766,10 @@ void launch_mfma(const LinearArgs& a, hipStream_t s) {
     const int64_t tiles = ((a.N + 15) / 16) * ((a.M + 15) / 16), cus = num_cus();
     // 16 < rows per CU <= 24 (QKV of the model: 6144 rows, 24 per CU): one
     // 24-row block per CU instead of 16-row tiles two to some CUs.
+    const int64_t nchunks = (a.K + kMfmaKC - 1) / kMfmaKC;
     if (EZ_MFMA_R2 && a.M <= 16 && a.N > 16 * cus && a.N <= 24 * cus) launch_mfma_r2<8>(a, s);
+    else if (EZ_MFMA_STREAM && (a.N + 15) / 16 >= 4 * cus && nchunks == 16 && a.K % kMfmaKC == 0)
+      launch_mfma_stream(a, cus, s);
     else if (tiles > cus && tiles <= 2 * cus) launch_mfma_nw<false, 4>(a, s);
     else launch_mfma_nw<false, 8>(a, s);
   }

@@ -405,3 +405,29 @@ def test_linear_stage_24_row_blocks(M, extra, K, epi):
         np.testing.assert_allclose(n(Y), ref, rtol=1e-3, atol=1e-3)
     else:
         np.testing.assert_allclose(n(Y), ref, **BF_TOL)
+
+
+@pytest.mark.parametrize("M,extra,epi", [(16, 37, 0), (5, 0, 1), (20, 1000, 3), (16, 8192, 1)])
+def test_linear_stage_streaming_blocks(M, extra, epi):
+    """At least four 16-row tiles per CU and K = 4096 (an LM head at batch
+    > 4): two streaming blocks per CU walk the tiles with one DMA ring;
+    ragged last tiles, partial batch blocks and every store form."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    N, K = 4 * 16 * cus + extra, 4096
+    rng = np.random.default_rng(M + N + epi)
+    X = oracle.bf16(rng.standard_normal((M, K)).astype(np.float32))
+    W = oracle.bf16(rng.standard_normal((N, K)).astype(np.float32) * K ** -0.5)
+    R = oracle.bf16(rng.standard_normal((M, N)).astype(np.float32))
+    g_ = oracle.linear_bf16(X, W)
+    ref = {0: g_, 1: oracle.bf16(R + g_), 3: X @ W.T}[epi]
+    tX, tW, tR = g(X), g(W), g(R)
+    Y = torch.full((M, N), float("nan"), dtype=torch.float32 if epi == 3 else torch.bfloat16, device=DEV)
+    ws = torch.zeros(256, dtype=torch.uint8, device=DEV)
+    for _ in range(2):  # the second call on the same output: bitwise the same
+        _hip.call("ezops_linear_stage_bf16", tX.data_ptr(), K, tW.data_ptr(), None, Y.data_ptr(), N,
+                  tR.data_ptr(), N, None, 0, 1e-6, epi, M, N, K, ws.data_ptr(), ws.numel(), _hip.stream())
+        torch.cuda.synchronize()
+        if epi == 3:
+            np.testing.assert_allclose(n(Y), ref, rtol=1e-3, atol=1e-3)
+        else:
+            np.testing.assert_allclose(n(Y), ref, **BF_TOL)
