@@ -278,6 +278,24 @@ __global__ __launch_bounds__(256) void probe_read_kernel(const f32x4v_t* __restr
   if (acc.x == 1234.5f) sink[0] = acc;  // keeps the loads alive; practically never stores
 }
 
+// One-shot streaming read: block b reads its own contiguous 32 KiB (every
+// load issued before any is used, non-temporal), the grid covering the
+// array, as the row-block GEMV reads a weight matrix.
+__global__ __launch_bounds__(256) void probe_read_blocks_kernel(const f32x4v_t* __restrict__ b, int64_t n4,
+                                                                f32x4v_t* __restrict__ sink) {
+  const int64_t base = int64_t(blockIdx.x) * 256 * kProbeUnroll + threadIdx.x;
+  f32x4v_t x[kProbeUnroll];
+#pragma unroll
+  for (int u = 0; u < kProbeUnroll; ++u) {
+    const int64_t j = base + u * 256;
+    x[u] = __builtin_nontemporal_load(b + (j < n4 ? j : n4 - 1));
+  }
+  f32x4v_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < kProbeUnroll; ++u) acc += x[u];
+  if (acc.x == 1234.5f) sink[0] = acc;  // keeps the loads alive; practically never stores
+}
+
 template <int KIND>  // 1 write, 2 copy, 3 triad
 __global__ __launch_bounds__(256) void probe_stream_kernel(f32x4v_t* __restrict__ a, const f32x4v_t* __restrict__ b,
                                                            const f32x4v_t* __restrict__ c, int64_t n4, float s) {
@@ -505,7 +523,7 @@ extern "C" int ezops_mfma_probe(int kind, float* out, int64_t blocks, int64_t it
 
 extern "C" int ezops_hbm_probe(int kind, float* a, const float* b, const float* c, int64_t n, float sc,
                                hipStream_t s) {
-  EZ_REQUIRE(kind >= 0 && kind <= 4, "hbm_probe: kind must be 0..4");
+  EZ_REQUIRE(kind >= 0 && kind <= 5, "hbm_probe: kind must be 0..5");
   EZ_REQUIRE(a && (kind == 1 || b) && (kind != 3 || c), "hbm_probe: null pointer");
   EZ_REQUIRE(n >= 4 && n % 4 == 0, "hbm_probe: n must be a positive multiple of 4");
   const dim3 grid{unsigned(num_cus() * 16), 1, 1}, block{256, 1, 1};
@@ -515,6 +533,12 @@ extern "C" int ezops_hbm_probe(int kind, float* a, const float* b, const float* 
   switch (kind) {
     case 0: hipLaunchKernelGGL(probe_read_kernel<0>, dim3(unsigned(num_cus() * 4)), block, 0, s, Bv, n / 4, A); break;
     case 4: hipLaunchKernelGGL(probe_read_kernel<1>, dim3(unsigned(num_cus() * 32)), block, 0, s, Bv, n / 4, A); break;
+    case 5: {
+      const int64_t blocks = (n / 4 + 256 * kProbeUnroll - 1) / (256 * kProbeUnroll);
+      EZ_REQUIRE(blocks < (int64_t(1) << 31), "hbm_probe: array too large for one-shot blocks");
+      hipLaunchKernelGGL(probe_read_blocks_kernel, dim3(unsigned(blocks)), block, 0, s, Bv, n / 4, A);
+      break;
+    }
     case 1: hipLaunchKernelGGL(probe_stream_kernel<1>, grid, block, 0, s, A, Bv, Cv, n / 4, sc); break;
     case 2: hipLaunchKernelGGL(probe_stream_kernel<2>, grid, block, 0, s, A, Bv, Cv, n / 4, sc); break;
     default: hipLaunchKernelGGL(probe_stream_kernel<3>, grid, block, 0, s, A, Bv, Cv, n / 4, sc); break;

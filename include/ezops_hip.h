@@ -335,7 +335,9 @@ int ezops_profile_reset(void);
  * (replaces benchmarks/hardware/memory/hbm_saturation.cu:49-90):
  * kind 0 = read (sum into out[0..]; allocates in the caches, used as the
  * cache flush), 1 = write, 2 = copy, 3 = triad a = b + s*c, 4 = streaming read
- * (non-temporal hint).  n = float count per array. */
+ * (non-temporal hint, 32 blocks per CU looping over the array), 5 = streaming
+ * read in one-shot blocks (each block reads its own contiguous 32 KiB, the
+ * grid covering the array).  n = float count per array. */
 int ezops_hbm_probe(int kind, float* a, const float* b, const float* c, int64_t n, float s,
                     hipStream_t stream);
 
