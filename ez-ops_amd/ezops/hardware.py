@@ -126,7 +126,7 @@ def generate_yaml(profile: str, gpu_name: str, hbm: dict, mfma_tflops: dict) -> 
     reads -- carries the fp32 matrix peak and its calibration."""
     spec = SPECS[profile]
     best = max(hbm.values())
-    src = "streaming read (non-temporal)" if "read" in hbm and hbm["read"] >= best else "STREAM Triad"
+    src = "streaming read (non-temporal, one-shot blocks)" if "read" in hbm and hbm["read"] >= best else "STREAM Triad"
     lines = [
         f"# GPU Profile: {gpu_name}",
         "# Calibration: ezops_hbm_probe (STREAM probes over 2 GiB arrays) and ezops_mfma_probe",
@@ -150,7 +150,7 @@ def generate_yaml(profile: str, gpu_name: str, hbm: dict, mfma_tflops: dict) -> 
     if "triad" in hbm:
         lines.append(f"  triad_calibration: {hbm['triad'] / spec['hbm_bw_gb']:.3f}   # STREAM Triad")
     if "read" in hbm:
-        lines.append(f"  read_calibration: {hbm['read'] / spec['hbm_bw_gb']:.3f}    # streaming read (non-temporal)")
+        lines.append(f"  read_calibration: {hbm['read'] / spec['hbm_bw_gb']:.3f}    # streaming read (non-temporal, one-shot blocks)")
     lines += ["", "tensor_core:"]
     entries = dict(spec["tensor_core_tflops"])
     entries["tf32"] = entries["fp32"]
