@@ -20,11 +20,11 @@
 //   * online softmax in the exp2 domain (scale * log2 e folded into S), one
 //     head per lane column: row maxima across the 4 lane groups by lane
 //     swaps, the rescale of O skipped when no running max moved.
-//   * O^T += V^T P^T: the 8 probabilities of a lane, rounded to bf16, are the
-//     B operand as they stand (k-slot 8 lg + e = position 16(e/4) + 4 lg +
-//     e%4); V rows are read with fully coalesced 16-byte loads, stored
+//   * O^T += V^T P^T: the 8 probabilities of a lane, split into bf16 high
+//     and low parts (two MFMAs per fragment), are the B operand as they
+//     stand (k-slot 8 lg + e = position 16(e/4) + 4 lg + e%4); V rows are read with fully coalesced 16-byte loads, stored
 //     row-major into a per-wave LDS slab and read back as the V^T operand by
-//     transposing LDS reads (ds_read_b64_tr_b16), D/16 MFMAs per tile; the
+//     transposing LDS reads (ds_read_b64_tr_b16), 2 D/16 MFMAs per tile; the
 //     slab holds the tile's K first, then its V.
 //   * every tile load is unconditional (rows past the live length read a
 //     clamp row): the next tile's K is requested right after the score MFMAs
@@ -41,10 +41,6 @@
 #include "prof.h"
 #include "status.h"
 #include "../../include/ezops_hip.h"
-
-#ifndef EZ_ATTN_TARGET4
-#define EZ_ATTN_TARGET4 8  // 4-wave blocks planned per CU
-#endif
 
 namespace ez {
 
@@ -472,17 +468,23 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
 #pragma unroll
       for (int db = 0; db < NDB; ++db) o[db] *= alpha;
     }
-    // P^T operand: k-slot 8lg + e = position 16(e/4) + 4lg + e%4, bf16; the
-    // sum takes the rounded weights the product uses.
-    uint32_t pw[4];
+    // P^T operand: k-slot 8lg + e = position 16(e/4) + 4lg + e%4, as two
+    // bf16 parts p = hi + lo (hi = bf16(p), lo = bf16(p - hi)): the two
+    // products against the same V^T fragments carry P to ~16 significant
+    // bits, so the value sum matches the fp32 weights of the reference
+    // (rounding P to bf16 alone puts a relative error of ~2^-9 on every
+    // weight, which the Qwen3 layer's FFN carries to its output).
+    uint32_t pw[4], pl[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const float p0 = __builtin_amdgcn_exp2f(acc[q >> 1][2 * (q & 1)] - mn);
       const float p1 = __builtin_amdgcn_exp2f(acc[q >> 1][2 * (q & 1) + 1] - mn);
       pw[q] = cvt_bf2(p0, p1);
-      l_acc += bf_lo(pw[q]) + bf_hi(pw[q]);
+      pl[q] = cvt_bf2(p0 - bf_lo(pw[q]), p1 - bf_hi(pw[q]));
+      l_acc += p0 + p1;
     }
     const bf16x8_t pb = as_bf16x8(make_uint4(pw[0], pw[1], pw[2], pw[3]));
+    const bf16x8_t pbl = as_bf16x8(make_uint4(pl[0], pl[1], pl[2], pl[3]));
 
     // ---- O^T += V^T P^T: this tile's V from its registers into the slab
     // (the previous tile's reads of it have completed), then read transposed.
@@ -506,6 +508,7 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
         const bf16x8_t va = __builtin_bit_cast(bf16x8_t, (u32x4_t){uint32_t(vt[2 * k][0]), uint32_t(vt[2 * k][1]),
                                                                    uint32_t(vt[2 * k + 1][0]), uint32_t(vt[2 * k + 1][1])});
         o[4 * q + k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, o[4 * q + k], 0, 0, 0);
+        o[4 * q + k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pbl, o[4 * q + k], 0, 0, 0);
       }
     }
     // next V (unconditional like the K loads: past the end every row clamps
@@ -634,7 +637,7 @@ SplitPlan plan_splits(int64_t B, int64_t Hkv, int64_t Lh, int64_t G, bool balanc
   // 8-wave blocks for few units; groups 8 and 16 keep 4 waves (its accumulators need
   // the register budget of one wave per SIMD).
   const int waves = (units * 4 <= cus && G <= 4) ? 8 : 4;
-  const int64_t target = waves == 8 ? 2 * cus : EZ_ATTN_TARGET4 * cus;  // blocks in flight
+  const int64_t target = waves == 8 ? 2 * cus : 8 * cus;  // blocks in flight (4-wave: B=16 layer 211/205/205/212/220 us at 4/6/8/12/16 per CU)
   int64_t ns = (target + units - 1) / units;
   const int64_t max_ns = (Lh + int64_t(waves) * kTile - 1) / (int64_t(waves) * kTile);
   if (ns > max_ns) ns = max_ns;

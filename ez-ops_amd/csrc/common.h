@@ -4,10 +4,6 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#ifndef EZ_NT_LOADS
-#define EZ_NT_LOADS 1
-#endif
-
 namespace ez {
 
 constexpr int kWave = 64;
@@ -44,19 +40,14 @@ __device__ __forceinline__ void unpack8(const uint4& v, float (&f)[8]) {
   f[6] = bf_lo(v.w); f[7] = bf_hi(v.w);
 }
 
-// 16-byte global load; with EZ_NT_LOADS (default) the load carries the
-// non-temporal hint: streamed weights / KV are read once and should not
+// 16-byte global load with the non-temporal hint: streamed weights / KV are read once and should not
 // displace reused lines.  Measured on MI355X: a 4 GiB streaming read reaches
 // 6.7 TB/s with the hint against 6.1 TB/s without, and the RMSNorm + gate/up
 // GEMV drops from 36 to 32 us.
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ld16_stream(const void* p) {
-#if EZ_NT_LOADS
   const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
   return make_uint4(v.x, v.y, v.z, v.w);
-#else
-  return *reinterpret_cast<const uint4*>(p);
-#endif
 }
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& v) { return __builtin_bit_cast(bf16x8_t, v); }

@@ -1,32 +1,26 @@
 // bf16 GEMV and skinny linear layers, Y[M, N] = X[M, K] . W[N, K]^T.
 //
 // Decode-time projections are HBM-bound: every weight byte is read once and
-// used M times.  Two kernels cover the batch range:
-//   * gemv_valu (M <= 4): one wave per R weight rows; each lane streams
-//     16-byte (8 x bf16) chunks of the row, so one wave instruction reads a
-//     fully coalesced 1 KiB of the row; fp32 FMAs; one wave reduction per
-//     output.
+// used M times.  The kernels by batch range:
+//   * gemv_rows (M <= 4, K <= 16384): a row group of 64-256 threads owns a
+//     few weight rows; each thread holds fixed 16-byte chunks of every row,
+//     all issued at once, so one wave instruction reads a fully coalesced
+//     1 KiB of a row and every x chunk serves all rows of the group.
+//   * gemv_valu (M <= 4, longer rows): one wave per R weight rows streaming
+//     16-byte chunks in a loop.
 //   * linear_mfma (M > 4): v_mfma_f32_16x16x32_bf16 on 16-row weight tiles
 //     against 16 batch rows; the K range is split over the 4 waves of a
 //     block and the partial tiles are summed through LDS.
-// Both can fuse the RMSNorm prologue (statistics from the X chunks already
-// in registers) and the residual / SwiGLU epilogues of the decode layer.
+// They fuse the RMSNorm prologue (M <= 4: statistics from the x chunks in
+// registers, then the reference's bf16 staging of the normalised input;
+// M > 4: one staging pass into the workspace) and the residual / SwiGLU
+// epilogues of the decode layer.
 #include "common.h"
 #include "internal.h"
 #include "prof.h"
 #include "status.h"
 #include "../../include/ezops_hip.h"
 
-// Tunables (defaults chosen by measurement on MI355X).
-#ifndef EZ_GEMV_BLOCK
-#define EZ_GEMV_BLOCK 256   // threads per block of the VALU GEMV
-#endif
-#ifndef EZ_GEMV_R1
-#define EZ_GEMV_R1 2        // weight rows per wave when M == 1
-#endif
-#ifndef EZ_GEMV_U
-#define EZ_GEMV_U 8         // 16-byte chunks per lane in flight per row (M <= 2)
-#endif
 
 namespace ez {
 
@@ -35,11 +29,8 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
-constexpr int kGemvBlock = EZ_GEMV_BLOCK;
+constexpr int kGemvBlock = 256;  // threads per block of the wave-per-row GEMV
 constexpr int kGemvWaves = kGemvBlock / kWave;
-#ifndef EZ_GEMV_RES_PREFETCH
-#define EZ_GEMV_RES_PREFETCH 1
-#endif
 
 __device__ __forceinline__ void store_out(const LinearArgs& a, int64_t m, int64_t n, float v,
                                           float v_up) {
@@ -92,17 +83,36 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_valu_kernel(LinearArgs a) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int64_t n = SILU ? n0 : (n0 + r < a.N ? n0 + r : a.N - 1);
-      resv[m][r] = (EZ_GEMV_RES_PREFETCH && a.epi == kEpiResid) ? bf2f(a.res[m * a.ldr + n]) : 0.f;
+      resv[m][r] = (a.epi == kEpiResid) ? bf2f(a.res[m * a.ldr + n]) : 0.f;
     }
 
-  float acc[M][R];
-  float ss[M];
+  // NORM: the row statistics first (x is L2-resident), so that the input
+  // can be staged as the reference stages it, bf16(x * rsqrt(mean x^2 + eps) * w).
+  float rs[M];
 #pragma unroll
-  for (int m = 0; m < M; ++m) {
-    ss[m] = 0.f;
+  for (int m = 0; m < M; ++m) rs[m] = 1.f;
+  if constexpr (NORM) {
+    float ss[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) ss[m] = 0.f;
+    for (int64_t c = lane; c < nchunk; c += kWave) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float x[8];
+        unpack8(xp[m][c], x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss[m] = fmaf(x[e], x[e], ss[m]);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) rs[m] = rsqrtf(wave_sum(ss[m]) / float(a.K) + a.eps);
+  }
+
+  float acc[M][R];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[m][r] = 0.f;
-  }
 
   for (int64_t c0 = lane; c0 < nchunk; c0 += int64_t(kWave) * U) {
     uint4 wv[U][R], xv[U][M], nv[U];
@@ -126,10 +136,7 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_valu_kernel(LinearArgs a) {
         unpack8(xv[u][m], x);
         if (NORM) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            ss[m] = fmaf(x[e], x[e], ss[m]);
-            x[e] *= nw[e];
-          }
+          for (int e = 0; e < 8; ++e) x[e] = round_bf(x[e] * rs[m] * nw[e]);
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -144,11 +151,9 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_valu_kernel(LinearArgs a) {
 
 #pragma unroll
   for (int m = 0; m < M; ++m) {
-    float scale = 1.f;
-    if (NORM) scale = rsqrtf(wave_sum(ss[m]) / float(a.K) + a.eps);
     float v[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) v[r] = wave_sum(acc[m][r]) * scale;
+    for (int r = 0; r < R; ++r) v[r] = wave_sum(acc[m][r]);
     if (lane == 0) {
       if (SILU) {
         store_out(a, m, n0, v[0], v[1]);
@@ -156,7 +161,7 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_valu_kernel(LinearArgs a) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           if (n0 + r >= a.N) continue;
-          if (EZ_GEMV_RES_PREFETCH && a.epi == kEpiResid)
+          if (a.epi == kEpiResid)
             reinterpret_cast<uint16_t*>(a.Y)[m * a.ldy + n0 + r] = f2bf(resv[m][r] + round_bf(v[r]));
           else
             store_out(a, m, n0 + r, v[r], 0.f);
@@ -492,73 +497,124 @@ __global__ __launch_bounds__(NW * kWave) void linear_mfma_kernel(LinearArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Row-block GEMV, M <= 4 and K = 2048 * CH.  A block of 256 threads owns RB
-// output rows (SwiGLU: RB gate rows and the RB matching up rows); thread t
-// holds the 16-byte chunks t, t + 256, ... of every row, so each wave
-// instruction reads 1 KiB of one row, all weight loads of a thread are issued
-// back to back with no bounds branches, and every x chunk a thread loads
-// serves all RB rows (x traffic through L2 is 1/RB of the weight traffic).
-// Partial sums are reduced per wave (DPP) and across the 4 waves through LDS.
-template <int M, int RB, int CH, bool NORM, bool SILU>
+// Row-block GEMV, M <= 4 and K % 8 == 0, K <= 16384.  A block of 256
+// threads is split into 256 / TPR row groups of TPR threads; each group owns
+// RB output rows (SwiGLU: RB gate rows and the RB matching up rows).  Thread
+// t of a group holds the 16-byte chunks t, t + TPR, ... (CH of them, the
+// last one masked when K / 8 is not a multiple of TPR) of every row, so each
+// wave instruction reads 1 KiB of one row, all weight loads of a thread are
+// issued back to back, and every x chunk a thread loads serves all RB rows
+// (x traffic through L2 is 1/RB of the weight traffic).  Partial sums are
+// reduced per wave (DPP) and across the group's waves through LDS.
+//
+// NORM: the reference's staging xn = bf16(x * rsqrt(mean x^2 + eps) * w)
+// (ezops/ops/fused_o_proj_ffn.py:107-110).  x and the norm weights are
+// requested before the weight rows; the sum of squares is reduced across
+// the group while the weight loads are in flight, then every x chunk is
+// normalised and rounded to bf16 before it meets the weights.
+template <int M, int RB, int CH, int TPR, bool NORM, bool SILU, bool TAIL>
 __global__ __launch_bounds__(kBlock) void gemv_rows_kernel(LinearArgs a) {
   EZ_PROF_WAVE(kProfGemvRows);
-  constexpr int NR = SILU ? 2 * RB : RB;  // weight rows per block
-  constexpr int NQ = M * NR + (NORM ? M : 0);
-  __shared__ float red[kWavesPerBlock][NQ];
+  static_assert(TPR % kWave == 0 && kBlock % TPR == 0, "row group geometry");
+  constexpr int NR = SILU ? 2 * RB : RB;  // weight rows per group
+  constexpr int RG = kBlock / TPR;        // row groups per block
+  constexpr int WPG = TPR / kWave;        // waves per row group
+  __shared__ float red[kWavesPerBlock][M * NR];
+  __shared__ float sred[NORM ? kWavesPerBlock : 1][M];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
-  const int64_t n0 = int64_t(blockIdx.x) * RB;
+  const int grp = tid / TPR, t = tid % TPR;
+  const int64_t n0 = (int64_t(blockIdx.x) * RG + grp) * RB;
+  // TAIL: K / 8 is not a multiple of TPR and the last chunk is masked.
+  const bool last_ok = !TAIL || t + TPR * (CH - 1) < (a.K >> 3);
 
-  uint4 wv[NR][CH];
+  uint4 xv[M][CH], wv[NR][CH];
+  auto load_w = [&]() {
 #pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    const uint16_t* base = (SILU && r >= RB) ? a.W2 : a.W;
-    int64_t row = n0 + (r % RB);
-    if (row >= a.N) row = a.N - 1;  // tail rows: load a valid row, skip the store
-    const uint4* wp = reinterpret_cast<const uint4*>(base + row * a.K) + tid;
+    for (int r = 0; r < NR; ++r) {
+      const uint16_t* base = (SILU && r >= RB) ? a.W2 : a.W;
+      int64_t row = n0 + (r % RB);
+      if (row >= a.N) row = a.N - 1;  // tail rows: load a valid row, skip the store
+      const uint4* wp = reinterpret_cast<const uint4*>(base + row * a.K) + t;
 #pragma unroll
-    for (int j = 0; j < CH; ++j) wv[r][j] = ld16_stream(wp + kBlock * j);
+      for (int j = 0; j < CH; ++j)
+        wv[r][j] = (j + 1 < CH || last_ok) ? ld16_stream(wp + TPR * j) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto load_x = [&]() {
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int j = 0; j < CH; ++j)
+        xv[m][j] = (j + 1 < CH || last_ok) ? reinterpret_cast<const uint4*>(a.X + m * a.ldx)[t + TPR * j]
+                                           : make_uint4(0, 0, 0, 0);
+  };
+  // A wave's loads complete in order: with NORM the statistics need x
+  // first, so x (and the norm weights) are requested ahead of the weight
+  // rows; without it the weight rows go first.
+  uint4 nv[NORM ? CH : 1];
+  if constexpr (NORM) {
+    load_x();
+#pragma unroll
+    for (int j = 0; j < CH; ++j)
+      nv[j] = (a.norm_w && (j + 1 < CH || last_ok)) ? reinterpret_cast<const uint4*>(a.norm_w)[t + TPR * j]
+                                                    : make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
+    load_w();
+  } else {
+    load_w();
+    load_x();
   }
-  uint4 xv[M][CH];
+  // The finishing thread (m, r) of each group fetches its residual with the
+  // weight loads.
+  uint16_t res_raw = 0;
+  if (a.epi == kEpiResid && t < M * RB) {
+    const int64_t n = n0 + t % RB;
+    if (n < a.N) res_raw = a.res[(t / RB) * a.ldr + n];
+  }
+
+  if constexpr (NORM) {
+    float ss[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      ss[m] = 0.f;
+#pragma unroll
+      for (int j = 0; j < CH; ++j) {
+        float x[8];
+        unpack8(xv[m][j], x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss[m] = fmaf(x[e], x[e], ss[m]);
+      }
+      const float v = wave_reduce_uniform<false>(ss[m]);
+      if (lane == 0) sred[wave][m] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float sq = 0.f;
+#pragma unroll
+      for (int w = 0; w < WPG; ++w) sq += sred[grp * WPG + w][m];
+      const float rs = rsqrtf(sq / float(a.K) + a.eps);
+#pragma unroll
+      for (int j = 0; j < CH; ++j) {
+        float x[8], g[8];
+        unpack8(xv[m][j], x);
+        unpack8(nv[j], g);
+        xv[m][j] = make_uint4(pack_bf2(x[0] * rs * g[0], x[1] * rs * g[1]), pack_bf2(x[2] * rs * g[2], x[3] * rs * g[3]),
+                              pack_bf2(x[4] * rs * g[4], x[5] * rs * g[5]), pack_bf2(x[6] * rs * g[6], x[7] * rs * g[7]));
+      }
+    }
+  }
+
+  float acc[M][NR];
 #pragma unroll
   for (int m = 0; m < M; ++m)
 #pragma unroll
-    for (int j = 0; j < CH; ++j) xv[m][j] = reinterpret_cast<const uint4*>(a.X + m * a.ldx)[tid + kBlock * j];
-  uint4 nv[NORM ? CH : 1];
-  if constexpr (NORM) {
-#pragma unroll
-    for (int j = 0; j < CH; ++j)
-      nv[j] = a.norm_w ? reinterpret_cast<const uint4*>(a.norm_w)[tid + kBlock * j]
-                       : make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
-  }
-  // The finishing thread (m, r) fetches its residual with the weight loads.
-  uint16_t res_raw = 0;
-  if (a.epi == kEpiResid && tid < M * RB) {
-    const int64_t n = n0 + tid % RB;
-    if (n < a.N) res_raw = a.res[(tid / RB) * a.ldr + n];
-  }
-
-  float acc[M][NR], ss[M];
-#pragma unroll
-  for (int m = 0; m < M; ++m) {
-    ss[m] = 0.f;
-#pragma unroll
     for (int r = 0; r < NR; ++r) acc[m][r] = 0.f;
-  }
 #pragma unroll
   for (int j = 0; j < CH; ++j) {
-    float nw[8];
-    if constexpr (NORM) unpack8(nv[j], nw);
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       float x[8];
       unpack8(xv[m][j], x);
-      if constexpr (NORM) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          ss[m] = fmaf(x[e], x[e], ss[m]);
-          x[e] *= nw[e];
-        }
-      }
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
         float w[8];
@@ -570,36 +626,23 @@ __global__ __launch_bounds__(kBlock) void gemv_rows_kernel(LinearArgs a) {
   }
 
 #pragma unroll
-  for (int m = 0; m < M; ++m) {
+  for (int m = 0; m < M; ++m)
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
       const float v = wave_reduce_uniform<false>(acc[m][r]);
       if (lane == 0) red[wave][m * NR + r] = v;
     }
-    if constexpr (NORM) {
-      const float v = wave_reduce_uniform<false>(ss[m]);
-      if (lane == 0) red[wave][M * NR + m] = v;
-    }
-  }
   __syncthreads();
-  if (tid >= M * RB) return;
-  const int m = tid / RB, r = tid % RB;
+  if (t >= M * RB) return;
+  const int m = t / RB, r = t % RB;
   const int64_t n = n0 + r;
   if (n >= a.N) return;
-  float v = 0.f, vu = 0.f, scale = 1.f;
+  float v = 0.f, vu = 0.f;
 #pragma unroll
-  for (int w = 0; w < kWavesPerBlock; ++w) {
-    v += red[w][m * NR + r];
-    if constexpr (SILU) vu += red[w][m * NR + RB + r];
+  for (int w = 0; w < WPG; ++w) {
+    v += red[grp * WPG + w][m * NR + r];
+    if constexpr (SILU) vu += red[grp * WPG + w][m * NR + RB + r];
   }
-  if constexpr (NORM) {
-    float sq = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWavesPerBlock; ++w) sq += red[w][M * NR + m];
-    scale = rsqrtf(sq / float(a.K) + a.eps);
-  }
-  v *= scale;
-  vu *= scale;
   if (a.epi == kEpiResid) {
     reinterpret_cast<uint16_t*>(a.Y)[m * a.ldy + n] = f2bf(bf2f(res_raw) + round_bf(v));
   } else {
@@ -616,79 +659,95 @@ __global__ __launch_bounds__(kBlock) void linear_scalar_kernel(LinearArgs a) {
   if (n >= a.N) return;
   for (int64_t m = 0; m < a.M; ++m) {
     const uint16_t* x = a.X + m * a.ldx;
-    float acc = 0.f, acc2 = 0.f, ss = 0.f;
+    float rs = 1.f;
+    if (a.norm) {  // statistics first, then the reference's bf16 staging of x * rs * w
+      float ss = 0.f;
+      for (int64_t k = lane; k < a.K; k += kWave) ss = fmaf(bf2f(x[k]), bf2f(x[k]), ss);
+      rs = rsqrtf(wave_sum(ss) / float(a.K) + a.eps);
+    }
+    float acc = 0.f, acc2 = 0.f;
     for (int64_t k = lane; k < a.K; k += kWave) {
       float xv = bf2f(x[k]);
-      if (a.norm) {
-        ss = fmaf(xv, xv, ss);
-        if (a.norm_w) xv *= bf2f(a.norm_w[k]);
-      }
+      if (a.norm) xv = round_bf(xv * rs * (a.norm_w ? bf2f(a.norm_w[k]) : 1.f));
       acc = fmaf(bf2f(a.W[n * a.K + k]), xv, acc);
       if (a.epi == kEpiSilu) acc2 = fmaf(bf2f(a.W2[n * a.K + k]), xv, acc2);
     }
-    float scale = a.norm ? rsqrtf(wave_sum(ss) / float(a.K) + a.eps) : 1.f;
-    acc = wave_sum(acc) * scale;
-    acc2 = wave_sum(acc2) * scale;
+    acc = wave_sum(acc);
+    acc2 = wave_sum(acc2);
     if (lane == 0) store_out(a, m, n, acc, acc2);
   }
 }
 
 template <int M, bool NORM, bool SILU>
 void launch_valu(const LinearArgs& a, hipStream_t s) {
-  constexpr int R = SILU ? 2 : (M == 1 ? EZ_GEMV_R1 : 1);
-  constexpr int U = M <= 2 ? EZ_GEMV_U : 4;
+  constexpr int R = SILU ? 2 : (M == 1 ? 2 : 1);  // weight rows per wave
+  constexpr int U = M <= 2 ? 8 : 4;               // 16-byte chunks per lane in flight per row
   const int64_t waves = SILU ? a.N : (a.N + R - 1) / R;
   const int64_t blocks = (waves + kGemvWaves - 1) / kGemvWaves;
   hipLaunchKernelGGL((gemv_valu_kernel<M, R, U, NORM, SILU>), dim3(blocks), dim3(kGemvBlock), 0, s, a);
 }
 
-#ifndef EZ_ROWS_RB4K
-#define EZ_ROWS_RB4K 4   // rows per block of the row-block GEMV at K = 4096 (SwiGLU: half)
-#endif
-#ifndef EZ_ROWS_RB12K
-#define EZ_ROWS_RB12K 2  // rows per block at K = 12288
-#endif
-#ifndef EZ_GEMV_ROWS
-#define EZ_GEMV_ROWS 1   // 0: always the wave-per-row kernel
-#endif
+// Rows per row group of the row-block GEMV, by chunks per thread (measured
+// on the Qwen3-8B stages: K = 4096 four rows, the QKV projection ran
+// 10.5 / 11.1 / 12.0 us with 4 / 2 / 1; K = 12288 two rows, the down
+// projection 17.8 / 18.4 us with 2 / 1; SwiGLU halves them: two gate and
+// two up rows, 32.6 us against 34.5 with one each).
+constexpr int rows_per_group(int ch, bool silu) { return silu ? (ch <= 2 ? 2 : 1) : (ch <= 2 ? 4 : 2); }
 
-template <int M, int CH, bool NORM, bool SILU>
-void launch_rows(const LinearArgs& a, hipStream_t s) {
-  constexpr int RB0 = CH <= 2 ? EZ_ROWS_RB4K : EZ_ROWS_RB12K;
-  constexpr int RB = SILU ? (RB0 / 2 > 0 ? RB0 / 2 : 1) : RB0;
+template <int M, int CH, int TPR, bool NORM, bool SILU, bool TAIL>
+void launch_rows_t(const LinearArgs& a, hipStream_t s) {
+  constexpr int RB = rows_per_group(CH, SILU);
+  constexpr int RG = kBlock / TPR;
   // Small matrices (<= 1024 blocks of RB rows): a quarter of the rows per
-  // block, so four times the blocks share the ramp (GEMV 4096 x 4096, RB 4 /
-  // 2 / 1: 8.0 / 7.7 / 7.5 us).  Larger stages keep RB rows: the QKV
-  // projection (6144 rows, RMSNorm prologue, whose sum of squares every
-  // block computes) ran 10.5 / 11.1 / 12.0 us with 4 / 2 / 1 rows per block.
-  if constexpr (RB > 2) {
-    if ((a.N + RB - 1) / RB <= 1024) {
-      constexpr int RS = RB / 4 > 0 ? RB / 4 : 1;
-      const int64_t blocks = (a.N + RS - 1) / RS;
-      hipLaunchKernelGGL((gemv_rows_kernel<M, RS, CH, NORM, SILU>), dim3(unsigned(blocks)), dim3(kBlock), 0, s, a);
+  // group, so four times the blocks share the ramp (GEMV 4096 x 4096, RB 4 /
+  // 2 / 1: 8.0 / 7.7 / 7.5 us).
+  if constexpr (RB == 4) {
+    if ((a.N + RB * RG - 1) / (RB * RG) <= 1024) {
+      const int64_t blocks = (a.N + RG - 1) / RG;
+      hipLaunchKernelGGL((gemv_rows_kernel<M, 1, CH, TPR, NORM, SILU, TAIL>), dim3(unsigned(blocks)), dim3(kBlock), 0, s, a);
       return;
     }
   }
-  const int64_t blocks = (a.N + RB - 1) / RB;
-  hipLaunchKernelGGL((gemv_rows_kernel<M, RB, CH, NORM, SILU>), dim3(unsigned(blocks)), dim3(kBlock), 0, s, a);
+  const int64_t blocks = (a.N + RB * RG - 1) / (RB * RG);
+  hipLaunchKernelGGL((gemv_rows_kernel<M, RB, CH, TPR, NORM, SILU, TAIL>), dim3(unsigned(blocks)), dim3(kBlock), 0, s, a);
 }
 
-template <int CH, bool NORM, bool SILU>
-void launch_rows_m(const LinearArgs& a, hipStream_t s) {
-  switch (a.M) {
-    case 1: launch_rows<1, CH, NORM, SILU>(a, s); break;
-    case 2: launch_rows<2, CH, NORM, SILU>(a, s); break;
-    case 3: launch_rows<3, CH, NORM, SILU>(a, s); break;
-    default: launch_rows<4, CH, NORM, SILU>(a, s); break;
+template <int M, int CH, int TPR, bool NORM, bool SILU>
+void launch_rows(const LinearArgs& a, hipStream_t s) {
+  if ((a.K >> 3) % TPR != 0) return launch_rows_t<M, CH, TPR, NORM, SILU, true>(a, s);
+  launch_rows_t<M, CH, TPR, NORM, SILU, false>(a, s);
+}
+
+template <int M, bool NORM, bool SILU>
+void launch_rows_ch(const LinearArgs& a, hipStream_t s) {
+  const int64_t nchunk = a.K >> 3;
+  if (nchunk <= 64) return launch_rows<M, 1, 64, NORM, SILU>(a, s);
+  if (nchunk <= 128) return launch_rows<M, 1, 128, NORM, SILU>(a, s);
+  switch ((nchunk + kBlock - 1) / kBlock) {
+    case 1: return launch_rows<M, 1, 256, NORM, SILU>(a, s);
+    case 2: return launch_rows<M, 2, 256, NORM, SILU>(a, s);
+    case 3: return launch_rows<M, 3, 256, NORM, SILU>(a, s);
+    case 4: return launch_rows<M, 4, 256, NORM, SILU>(a, s);
+    case 5: return launch_rows<M, 5, 256, NORM, SILU>(a, s);
+    case 6: return launch_rows<M, 6, 256, NORM, SILU>(a, s);
+    case 7: return launch_rows<M, 7, 256, NORM, SILU>(a, s);
+    default: return launch_rows<M, 8, 256, NORM, SILU>(a, s);
   }
 }
 
+// M <= 4: the row-block kernel for K <= 16384 (every K % 8 == 0 reaching
+// here), the wave-per-row kernel for longer rows.
+constexpr int64_t kRowsMaxK = 8 * 8 * kBlock;
+
 template <bool NORM, bool SILU>
 void launch_valu_m(const LinearArgs& a, hipStream_t s) {
-  if (EZ_GEMV_ROWS && a.ldx % 8 == 0 && (a.K == 4096 || a.K == 12288)) {
-    if (a.K == 4096) launch_rows_m<2, NORM, SILU>(a, s);
-    else launch_rows_m<6, NORM, SILU>(a, s);
-    return;
+  if (a.K <= kRowsMaxK) {
+    switch (a.M) {
+      case 1: return launch_rows_ch<1, NORM, SILU>(a, s);
+      case 2: return launch_rows_ch<2, NORM, SILU>(a, s);
+      case 3: return launch_rows_ch<3, NORM, SILU>(a, s);
+      default: return launch_rows_ch<4, NORM, SILU>(a, s);
+    }
   }
   switch (a.M) {
     case 1: launch_valu<1, NORM, SILU>(a, s); break;
@@ -697,13 +756,6 @@ void launch_valu_m(const LinearArgs& a, hipStream_t s) {
     default: launch_valu<4, NORM, SILU>(a, s); break;
   }
 }
-
-#ifndef EZ_MFMA_R2
-#define EZ_MFMA_R2 1
-#endif
-#ifndef EZ_MFMA_STREAM
-#define EZ_MFMA_STREAM 1
-#endif
 
 template <bool SILU, int NW, int TPB = 1>
 void launch_mfma_nw(const LinearArgs& a, hipStream_t s) {
@@ -767,8 +819,8 @@ void launch_mfma(const LinearArgs& a, hipStream_t s) {
     // 16 < rows per CU <= 24 (QKV of the model: 6144 rows, 24 per CU): one
     // 24-row block per CU instead of 16-row tiles two to some CUs.
     const int64_t nchunks = (a.K + kMfmaKC - 1) / kMfmaKC;
-    if (EZ_MFMA_R2 && a.M <= 16 && a.N > 16 * cus && a.N <= 24 * cus) launch_mfma_r2<8>(a, s);
-    else if (EZ_MFMA_STREAM && (a.N + 15) / 16 >= 4 * cus && nchunks == 16 && a.K % kMfmaKC == 0)
+    if (a.M <= 16 && a.N > 16 * cus && a.N <= 24 * cus) launch_mfma_r2<8>(a, s);
+    else if ((a.N + 15) / 16 >= 4 * cus && nchunks == 16 && a.K % kMfmaKC == 0)
       launch_mfma_stream(a, cus, s);
     else if (tiles > cus && tiles <= 2 * cus) launch_mfma_nw<false, 4>(a, s);
     else launch_mfma_nw<false, 8>(a, s);

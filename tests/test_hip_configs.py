@@ -6,10 +6,12 @@ times: the B=32 non-ragged attention grid, the 32768-wide softmax rows, the
 2^28 sum's full grid, QK-norm+RoPE at Qwen3-8B heads over a 32768-row cache
 and the batch-16 Qwen3-8B layer over a 16384-row cache.
 
-Bars: bf16 allclose(atol 2e-2, rtol 1e-2) against the fp32-accumulated
-oracle; softmax atol 1e-6 / rtol 1e-5 (SoftmaxOp.check); sum atol 1e-7 * n
-(ReduceOp.check) and 1e-5 relative to the fp64 sum; fused ops relative
-Frobenius < 1e-2 (the ops' own check).
+Bars: every bf16 output elementwise within allclose(atol 2e-2, rtol 1e-2)
+of the fp32-accumulated oracle AND the op's own check
+(GemvOp / AttnDecodeOp: allclose 1e-2 / 1e-2, ezops/ops/gemv.py:12-13 and
+ezops/ops/attn_decode.py:18-19 in the reference; the fused ops: relative
+Frobenius < 1e-2); softmax atol 1e-6 / rtol 1e-5 (SoftmaxOp.check); sum
+atol 1e-7 * n (ReduceOp.check) and 1e-5 relative to the fp64 sum.
 """
 
 import numpy as np
@@ -25,6 +27,19 @@ BF_TOL = dict(rtol=1e-2, atol=2e-2)
 DEV = "cuda"
 
 
+def assert_layer_bar(out, ref):
+    """The Qwen3 layer: the elementwise bar on all but at most max(2, 1e-4 n)
+    elements, and every element within twice the bar.  Legitimate fp32
+    accumulation orders of the oracle itself already put an element of
+    config L (B=16) past the bar (bf16 staging flips carried through the
+    layer; tests/test_oracle.py::test_layer_bar_order_sensitivity), so no
+    implementation can be held to the bar on every element there."""
+    d = np.abs(out - ref)
+    bar = BF_TOL["atol"] + BF_TOL["rtol"] * np.abs(ref)
+    assert (d <= 2 * bar).all(), float((d - 2 * bar).max())
+    assert int((d > bar).sum()) <= max(2, int(1e-4 * d.size)), int((d > bar).sum())
+
+
 def n(x):
     return x.detach().float().cpu().numpy()
 
@@ -34,7 +49,9 @@ def test_config_g_gemv():
     op = GemvOp(4096, 4096, backend="hip")
     y = torch.empty(4096, dtype=torch.bfloat16, device=DEV)
     op(x, W, y)
-    np.testing.assert_allclose(n(y), oracle.gemv(n(x), n(W)), **BF_TOL)
+    ref = oracle.gemv(n(x), n(W))
+    np.testing.assert_allclose(n(y), ref, **BF_TOL)
+    assert op.check(y, torch.from_numpy(ref).to(torch.bfloat16).to(DEV))
 
 
 def test_config_n_rmsnorm():
@@ -78,6 +95,7 @@ def test_config_a_gqa_decode_b32():
     assert out.shape == (32, 32, 1, 128)
     ref = oracle.attn_decode(n(Q)[:, :, 0], n(K), n(V))
     np.testing.assert_allclose(n(out)[:, :, 0], ref, **BF_TOL)
+    assert op.check(out, torch.from_numpy(ref[:, :, None]).to(torch.bfloat16).to(DEV))
     assert torch.equal(out, op(Q, K, V))
 
 
@@ -110,8 +128,10 @@ def test_config_f2_o_proj_ffn(B):
     args = workloads.config_f2(B, DEV)
     op = FusedOProjFfnOp(B, 4096, 12288, 32, 128, backend="hip")
     out = op(*args)
-    ref = torch.from_numpy(oracle.o_proj_ffn(*[n(x) for x in args])).to(DEV)
+    ref_np = oracle.o_proj_ffn(*[n(x) for x in args])
+    ref = torch.from_numpy(ref_np).to(DEV)
     assert op.check(out, ref), (out.float() - ref).norm().item() / ref.norm().item()
+    np.testing.assert_allclose(n(out), ref_np, **BF_TOL)
 
 
 @pytest.mark.parametrize("B", [1, 16])
@@ -126,6 +146,7 @@ def test_config_l_qwen3_layer(B):
                                      cos=npy[11], sin=npy[12])
     ref_t = torch.from_numpy(ref).to(DEV)
     assert op.check(out, ref_t), (out.float() - ref_t).norm().item() / ref_t.norm().item()
+    assert_layer_bar(n(out), ref)
     Kc, Vc = data[1], data[2]
     for b, L in enumerate(lens):
         np.testing.assert_allclose(n(Kc[b, :, L - 1]), rK[b, :, L - 1], **BF_TOL)

@@ -15,6 +15,17 @@ from ezops import FusedOProjFfnOp, FusedQkNormRopeOp, Qwen3DenseDecodeOp, list_b
 pytestmark = pytest.mark.gpu
 BF_TOL = dict(rtol=1e-2, atol=2e-2)
 
+
+def assert_layer_bar(out, ref):
+    """The elementwise bar on all but at most max(2, 1e-4 n) elements, every
+    element within twice the bar: legitimate fp32 accumulation orders of the
+    oracle already differ past the bar on single elements of the Qwen3-8B
+    layer (tests/test_oracle.py::test_layer_bar_order_sensitivity)."""
+    d = np.abs(out - ref)
+    bar = BF_TOL["atol"] + BF_TOL["rtol"] * np.abs(ref)
+    assert (d <= 2 * bar).all(), float((d - 2 * bar).max())
+    assert int((d > bar).sum()) <= max(2, int(1e-4 * d.size)), int((d > bar).sum())
+
 QWEN3_VL_2B_HEADS = dict(num_heads=16, head_dim=128, num_kv_heads=8)
 QWEN3_VL_2B = dict(hidden_size=2048, intermediate_size=6144, num_heads=16, head_dim=128)
 QWEN3_0_6B = dict(hidden_size=1024, intermediate_size=3072, num_heads=16, head_dim=128)
@@ -77,7 +88,7 @@ def test_fused_o_proj_ffn(batch, shape):
     out = op(*data)
     ref = torch.from_numpy(oracle.o_proj_ffn(*[n(x) for x in data])).to(out.device)
     assert op.check(out, ref), (out.float() - ref).norm().item() / ref.norm().item()
-    np.testing.assert_allclose(n(out), n(ref), rtol=5e-2, atol=1e-1)
+    np.testing.assert_allclose(n(out), n(ref), **BF_TOL)
 
 
 def _layer(batch, seq_len, kwargs, **mode):
@@ -96,6 +107,7 @@ def _layer(batch, seq_len, kwargs, **mode):
                                      kv_lens=mode.get("kv_lens"), **extra)
     ref_t = torch.from_numpy(ref).to(out.device)
     assert op.check(out, ref_t), (out.float() - ref_t).norm().item() / ref_t.norm().item()
+    assert_layer_bar(n(out), ref)
     Kc, Vc = data[1], data[2]
     for b, L in enumerate(op.lens()):
         np.testing.assert_allclose(n(Kc[b, :, L - 1]), rK[b, :, L - 1], **BF_TOL)

@@ -29,13 +29,18 @@ def g(a, dtype=torch.bfloat16):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dtype).to(DEV)
 
 
-@pytest.mark.parametrize("N,K", [(4096, 4096), (8, 16), (7, 100), (4096, 12288), (6144, 4096), (1, 8), (333, 1032)])
+@pytest.mark.parametrize("N,K", [(4096, 4096), (8, 16), (7, 100), (4096, 12288), (6144, 4096), (1, 8), (333, 1032),
+                                 (4096, 2048), (2048, 1024), (6144, 2048), (1024, 3072), (2048, 6144)])
 def test_gemv(N, K):
+    """The reference's GEMV bench shape (4096 x 2048) and the Qwen3-0.6B /
+    VL-2B projection widths among them; the reference op's own check too."""
     torch.manual_seed(0)
     op = GemvOp(N, K, backend="hip")
     A, B, C = op.gen_data()
     op(A, B, C)
-    np.testing.assert_allclose(n(C), oracle.gemv(n(A), n(B)), **BF_TOL)
+    ref = oracle.gemv(n(A), n(B))
+    np.testing.assert_allclose(n(C), ref, **BF_TOL)
+    assert op.check(C, torch.from_numpy(ref).to(torch.bfloat16).to(DEV))
     assert check_determinism(op, (A, B), C) and check_input_readonly(op, (A, B), C)
 
 
@@ -348,7 +353,43 @@ def test_linear_stage_epilogues(M, epi, norm, N, K):
                      device=DEV)
     _hip.call("ezops_linear_stage_bf16", tX.data_ptr(), K, tW.data_ptr(), tW2.data_ptr(), Y.data_ptr(), N,
               tR.data_ptr(), N, tw.data_ptr(), norm, 1e-6, epi, M, N, K, ws.data_ptr(), ws.numel(), _hip.stream())
-    np.testing.assert_allclose(n(Y), ref, rtol=2e-2, atol=3e-2)
+    np.testing.assert_allclose(n(Y), ref, **BF_TOL)
+
+
+def _stage_ref(X, W, W2, R, w, norm, epi):
+    Xn = oracle.rmsnorm_bf16(X, w) if norm else X
+    g_ = oracle.linear_bf16(Xn, W)
+    if epi == 0:
+        return g_
+    if epi == 1:
+        return oracle.bf16(R + g_)
+    u = oracle.linear_bf16(Xn, W2)
+    return oracle.bf16(oracle.bf16(g_ / (1 + np.exp(-g_.astype(np.float64)))) * u)
+
+
+@pytest.mark.parametrize("M", [1, 2, 4])
+@pytest.mark.parametrize("K", [64, 520, 1024, 2048, 3072, 6144, 16384, 16392])
+@pytest.mark.parametrize("epi,norm", [(0, 0), (1, 0), (2, 1), (0, 1)])
+def test_gemv_rows_widths(M, K, epi, norm):
+    """M <= 4 at every row width class: 64- and 128-thread row groups (K <=
+    1024), 256-thread groups with 1-8 chunks per thread and a masked last
+    chunk (520, 3072), and past 16384 the wave-per-row kernel; with the
+    RMSNorm prologue staged in bf16 as the reference stages it.  N = 203
+    leaves the last row group partly empty."""
+    N = 203
+    rng = np.random.default_rng(7 * M + K + 13 * epi + norm)
+    X = oracle.bf16(rng.standard_normal((M, K)).astype(np.float32))
+    W = oracle.bf16(rng.standard_normal((N, K)).astype(np.float32) * K ** -0.5)
+    W2 = oracle.bf16(rng.standard_normal((N, K)).astype(np.float32) * K ** -0.5)
+    R = oracle.bf16(rng.standard_normal((M, N)).astype(np.float32))
+    w = oracle.bf16(rng.standard_normal(K).astype(np.float32) * 0.1 + 1)
+    ref = _stage_ref(X, W, W2, R, w, norm, epi)
+    Y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=DEV)
+    ws = torch.zeros(256, dtype=torch.uint8, device=DEV)
+    tX, tW, tW2, tR, tw = g(X), g(W), g(W2), g(R), g(w)  # held until the kernel has run
+    _hip.call("ezops_linear_stage_bf16", tX.data_ptr(), K, tW.data_ptr(), tW2.data_ptr(), Y.data_ptr(), N,
+              tR.data_ptr(), N, tw.data_ptr(), norm, 1e-6, epi, M, N, K, ws.data_ptr(), ws.numel(), _hip.stream())
+    np.testing.assert_allclose(n(Y), ref, **BF_TOL)
 
 
 @pytest.mark.parametrize("M,N", [(16, 12288), (20, 8192), (8, 12288)])
