@@ -65,7 +65,7 @@ def build(jobs: int | None = None, verbose: bool = True, extra_flags: tuple = ()
     tmp = lib.with_suffix(".so.tmp")
     rocm_lib = Path(hipcc()).resolve().parent.parent / "lib"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), f"-L{rocm_lib}",
-           f"-Wl,-rpath,{rocm_lib}", "-lhipblaslt", "-o", str(tmp)]
+           f"-Wl,-rpath,{rocm_lib}", "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}{r.stderr}")

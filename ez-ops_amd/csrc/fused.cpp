@@ -263,7 +263,6 @@ extern "C" int ezops_qwen3_decode_step_bf16(const ezops_qwen3_layer* layers, int
 namespace {
 struct PrefillBufs {
   uint16_t *xn, *qkv, *att, *h, *gu, *act;
-  void* gemm_ws;
 };
 size_t prefill_ws(const ezops_qwen3_layer* p, int64_t T, PrefillBufs* b, char* base) {
   const int64_t QR = p->H * p->D, QKV = QR + 2 * p->Hkv * p->D;
@@ -276,7 +275,6 @@ size_t prefill_ws(const ezops_qwen3_layer* p, int64_t T, PrefillBufs* b, char* b
   t.h = take(T * p->HS);
   t.gu = take(T * 2 * p->IS);
   t.act = take(T * p->IS);
-  t.gemm_ws = c.take<char>(kGemmWorkspace);
   if (b) *b = t;
   return size_t(c.p - base);
 }
@@ -308,7 +306,7 @@ extern "C" int ezops_qwen3_prefill_bf16(const ezops_qwen3_layer* p, int64_t T, c
   auto W = [](const void* q) { return static_cast<const uint16_t*>(q); };
 
   int rc = ezops_rmsnorm_bf16(hidden, p->in_norm_w, w.xn, T, HS, p->eps, s);
-  if (!rc) rc = gemm_bf16(w.xn, HS, W(p->Wqkv), w.qkv, QKV, nullptr, T, QKV, HS, w.gemm_ws, kGemmWorkspace, s);
+  if (!rc) rc = gemm_bf16(w.xn, HS, W(p->Wqkv), w.qkv, QKV, nullptr, T, QKV, HS, s);
   if (rc) return rc;
 
   QkRopeArgs r{};
@@ -339,18 +337,17 @@ extern "C" int ezops_qwen3_prefill_bf16(const ezops_qwen3_layer* p, int64_t T, c
   a.B = p->B; a.T = T; a.H = p->H; a.Hkv = p->Hkv; a.S = p->S; a.D = p->D; a.max_q = max_q_len;
   a.scale = 0.f;
   rc = launch_prefill_attn(a, s);
-  if (!rc) rc = gemm_bf16(w.att, QR, W(p->Wo), w.h, HS, hidden, T, HS, QR, w.gemm_ws, kGemmWorkspace, s);
+  if (!rc) rc = gemm_bf16(w.att, QR, W(p->Wo), w.h, HS, hidden, T, HS, QR, s);
   if (!rc) rc = ezops_rmsnorm_bf16(w.h, p->post_norm_w, w.xn, T, HS, p->eps, s);
   if (!rc) {
     if (gemm_swiglu_supported(w.xn, HS, W(p->Wgu), w.act, IS, T, IS, HS)) {
       rc = gemm_swiglu(w.xn, HS, W(p->Wgu), w.act, IS, T, IS, HS, s);
     } else {
-      rc = gemm_bf16(w.xn, HS, W(p->Wgu), w.gu, 2 * IS, nullptr, T, 2 * IS, HS, w.gemm_ws, kGemmWorkspace, s);
+      rc = gemm_bf16(w.xn, HS, W(p->Wgu), w.gu, 2 * IS, nullptr, T, 2 * IS, HS, s);
       if (!rc) rc = launch_silu_mul(w.gu, w.act, T, IS, s);
     }
   }
   if (!rc)
-    rc = gemm_bf16(w.act, IS, W(p->Wd), static_cast<uint16_t*>(p->out), HS, w.h, T, HS, IS, w.gemm_ws,
-                   kGemmWorkspace, s);
+    rc = gemm_bf16(w.act, IS, W(p->Wd), static_cast<uint16_t*>(p->out), HS, w.h, T, HS, IS, s);
   return rc;
 }

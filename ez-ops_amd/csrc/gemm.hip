@@ -216,6 +216,16 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) 
     }
     frag_wait(fr);
   };
+  // The last K-step of K % 64 != 0: the 16-byte pieces at or past K hold
+  // the next row's elements (or zeros past the buffer); both operands'
+  // pieces there are zeroed, so they add nothing.
+  auto mask_tail = [&](int64_t k0) {
+#pragma unroll
+    for (int s = 0; s < kGK / 16; ++s)
+      if (k0 + (2 * s + h) * 8 >= a.K)
+#pragma unroll
+        for (int f = 0; f < FS; ++f) fr[FS * s + f] = u32x4v_t{0u, 0u, 0u, 0u};
+  };
   auto mult_step = [&]() {
 #pragma unroll
     for (int s = 0; s < kGK / 16; ++s)
@@ -233,7 +243,8 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) 
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  const int64_t nk = a.K / kGK;
+  const int64_t nk = (a.K + kGK - 1) / kGK;
+  const bool ktail = a.K % kGK != 0;
   // Steps 0 and 1 in flight before the loop (group 1 owns W of step 1).
   if (g == 0) {
     dma_x(0, 0);
@@ -247,6 +258,7 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) 
   for (int64_t j = 0; j < nk; ++j) {
     const int buf = int(j & 1);
     read_step(buf);
+    if (ktail && j + 1 == nk) mask_tail(j * kGK);
     if (g == 0) {
       if (j + 1 < nk) dma_x((j + 1) * kGK, buf ^ 1);
     } else if (j + 2 < nk) {
@@ -346,13 +358,13 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2))) 
 
 bool gemm_mfma_supported(const uint16_t* X, int64_t ldx, const uint16_t* W, const uint16_t* Y, int64_t ldy,
                          const uint16_t* R, int64_t M, int64_t N, int64_t K) {
-  (void)Y;
-  (void)ldy;
-  (void)R;
+  (void)R;  // R shares Y's leading dimension
   auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  // 16-byte pieces of K-rows (K % 8 == 0; the last K-step may be partial);
   // the DMA addresses operands by 32-bit byte offsets from their base
-  return K % kGK == 0 && ldx % 8 == 0 && al16(X) && al16(W) && M >= 1 && N >= 1 &&
-         (M - 1) * ldx * 2 + K * 2 < (int64_t(1) << 31) && (N - 1) * K * 2 + K * 2 < (int64_t(1) << 31);
+  return X && W && Y && M >= 1 && N >= 1 && K >= 8 && K % 8 == 0 && ldx >= K && ldx % 8 == 0 && ldy >= N &&
+         al16(X) && al16(W) && (M - 1) * ldx * 2 + K * 2 + kGK * 2 < (int64_t(1) << 31) &&
+         (N - 1) * K * 2 + K * 2 + kGK * 2 < (int64_t(1) << 31);
 }
 
 int gemm_mfma(const uint16_t* X, int64_t ldx, const uint16_t* W, uint16_t* Y, int64_t ldy, const uint16_t* R,
@@ -377,17 +389,47 @@ int gemm_mfma(const uint16_t* X, int64_t ldx, const uint16_t* W, uint16_t* Y, in
 bool gemm_swiglu_supported(const uint16_t* X, int64_t ldx, const uint16_t* W, const uint16_t* Y, int64_t ldy,
                            int64_t M, int64_t IS, int64_t K) {
   auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-  return IS % (kGN / 2) == 0 && ldy % 8 == 0 && al16(Y) && ldy >= IS &&
-         gemm_mfma_supported(X, ldx, W, Y, ldy, nullptr, M, 2 * IS, K);
+  return IS >= 1 && IS % (kGN / 2) == 0 && ldy % 8 == 0 && al16(Y) && ldy >= IS &&
+         gemm_mfma_supported(X, ldx, W, Y, 2 * IS, nullptr, M, 2 * IS, K);
 }
 
 int gemm_swiglu(const uint16_t* X, int64_t ldx, const uint16_t* W, uint16_t* Y, int64_t ldy, int64_t M, int64_t IS,
                 int64_t K, hipStream_t s) {
   EZ_REQUIRE(gemm_swiglu_supported(X, ldx, W, Y, ldy, M, IS, K),
-             "gemm_swiglu: shape or alignment not supported (IS % 128, K % 64, 16-byte rows)");
+             "gemm_swiglu: shape or alignment not supported (IS %% 128, K %% 8, ldx >= K, 16-byte rows)");
   GemmArgs a{X, ldx, W, Y, ldy, nullptr, M, 2 * IS, K, int((M + kGM - 1) / kGM), int(IS / (kGN / 2)), IS};
   hipLaunchKernelGGL((gemm_bf16_kernel<true, 2>), dim3(unsigned(a.tm * a.tn)), dim3(kGThreads), 0, s, a);
   return launch_status("gemm_swiglu (MFMA)");
 }
 
+// Prefill GEMM entry: the MFMA kernel for 16-byte K-rows (K % 8 == 0,
+// aligned operands); any other shape runs the linear-layer kernels of
+// gemv.hip (the residual epilogue rounds as here: bf16(R + bf16(X W^T))).
+int gemm_bf16(const uint16_t* X, int64_t ldx, const uint16_t* W, uint16_t* Y, int64_t ldy, const uint16_t* R,
+              int64_t M, int64_t N, int64_t K, hipStream_t s) {
+  EZ_REQUIRE(X && W && Y, "gemm: null pointer");
+  EZ_REQUIRE(M >= 1 && N >= 1 && K >= 1 && ldx >= K && ldy >= N, "gemm: bad shape");
+  if (gemm_mfma_supported(X, ldx, W, Y, ldy, R, M, N, K)) return gemm_mfma(X, ldx, W, Y, ldy, R, M, N, K, s);
+  LinearArgs l{};
+  l.X = X; l.ldx = ldx; l.W = W; l.Y = Y; l.ldy = ldy; l.M = M; l.N = N; l.K = K;
+  l.res = R; l.ldr = ldy; l.epi = R ? kEpiResid : kEpiStore;
+  return launch_linear(l, s);
+}
+
 }  // namespace ez
+
+extern "C" size_t ezops_gemm_workspace_size(void) { return 0; }
+
+extern "C" int ezops_gemm_swiglu_bf16(const void* X, int64_t ldx, const void* Wgu, void* Y, int64_t ldy, int64_t M,
+                                      int64_t IS, int64_t K, hipStream_t stream) {
+  return ez::gemm_swiglu(static_cast<const uint16_t*>(X), ldx, static_cast<const uint16_t*>(Wgu),
+                         static_cast<uint16_t*>(Y), ldy, M, IS, K, stream);
+}
+
+extern "C" int ezops_gemm_bf16(const void* X, int64_t ldx, const void* W, void* Y, int64_t ldy, const void* R,
+                               int64_t M, int64_t N, int64_t K, void* ws, size_t ws_bytes, hipStream_t stream) {
+  (void)ws;  // no workspace: kept for the ABI
+  (void)ws_bytes;
+  return ez::gemm_bf16(static_cast<const uint16_t*>(X), ldx, static_cast<const uint16_t*>(W),
+                       static_cast<uint16_t*>(Y), ldy, static_cast<const uint16_t*>(R), M, N, K, stream);
+}

@@ -497,6 +497,235 @@ __global__ __launch_bounds__(NW * kWave) void linear_mfma_kernel(LinearArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// X-stationary skinny GEMM (M > 4, K = 1024 * CPW): the linear_mfma layout
+// (4 waves split K, weight tiles landed in LDS by DMA through a per-wave
+// two-stage ring, v_mfma_f32_16x16x32_bf16) with each wave's K slice of the
+// 16 batch rows loaded into registers once, before the ring starts, and
+// kept for every tile the block walks (TPB tiles: blockIdx.x + k * gridDim.x;
+// R2 > 0: one block of 16 + R2 rows, as in linear_mfma).  X is read once
+// per block instead of once per tile.
+//
+// NORM: the RMSNorm prologue inside the kernel.  X is row-major; each lane
+// (row i, k-group g) sums the squares of its stationary elements, the four
+// lanes of a row and then the four waves (through LDS) complete the row's
+// statistics, and every fragment becomes bf16(x * rsqrt(mean x^2 + eps) * w)
+// -- the reference's staging (ezops/ops/fused_o_proj_ffn.py:107-110) --
+// as its chunk is first used (the norm weights through LDS), while the ring
+// streams on.  This replaces the separate staging pass of the batched path.
+template <int T, bool SILU, int CPW, int TPB, int R2, bool NORM>
+__global__ __launch_bounds__(4 * kWave) void linear_xs_kernel(LinearArgs a) {
+  constexpr int NW = 4;
+  static_assert(CPW > 0 && CPW % 2 == 0 && TPB >= 1, "unrolled even ring");
+  static_assert(R2 == 0 || (T == 2 && !SILU && TPB == 1 && R2 % 2 == 0 && R2 <= 16), "R2: two row tiles");
+  constexpr int kRowsPerBlock = R2 ? 16 + R2 : 16;
+  EZ_PROF_WAVE(kProfLinearMfma);
+  constexpr int DN = R2 ? kMfmaSlices + R2 / 2 : T * kMfmaSlices;  // DMA slices per chunk
+  constexpr int NC = TPB * CPW;
+  constexpr int kNormW = 4 * CPW * kMfmaKC / 8 / (NW * kWave);    // 16-byte norm-weight pieces per thread
+  __shared__ __align__(16) uint4 Wl0[NW][T][kMfmaSlices][kWave];
+  __shared__ __align__(16) uint4 Wl1[NW][T][kMfmaSlices][kWave];
+  __shared__ float red[NW][T][4][kWave];
+  __shared__ float nst[16][NW];
+  __shared__ uint4 wl[NORM ? NW * CPW * kMfmaKC / 8 : 1];  // the norm weights (K bf16)
+
+  const int lane = threadIdx.x & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int i = lane & 15, g = lane >> 4;
+  const int64_t m0 = int64_t(blockIdx.y) * 16;
+  const int64_t m = m0 + i;
+  const int64_t row0 = int64_t(blockIdx.x) * kRowsPerBlock;
+  const int64_t stride = int64_t(gridDim.x) * 16;
+
+  const int dr = lane >> 5, cs = lane & 31;
+  __amdgpu_buffer_rsrc_t wres0, wres1;
+  uint32_t woff[kMfmaSlices];
+  auto set_rows = [&](int64_t r0) {
+    const int64_t rows = a.N - r0 < 16 ? a.N - r0 : 16;
+    wres0 = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.W + r0 * a.K), 0, int(rows * a.K * 2),
+                                              0x00020000);
+    if constexpr (R2 > 0) {
+      const int64_t rows1 = a.N - r0 - 16 < R2 ? (a.N - r0 - 16 > 0 ? a.N - r0 - 16 : 0) : R2;
+      wres1 = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.W + (rows1 ? r0 + 16 : 0) * a.K), 0,
+                                                int(rows1 * a.K * 2), 0x00020000);
+    } else {
+      wres1 = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>((SILU ? a.W2 : a.W) + r0 * a.K), 0,
+                                                int(rows * a.K * 2), 0x00020000);
+    }
+#pragma unroll
+    for (int q = 0; q < kMfmaSlices; ++q) {
+      int64_t row = 2 * q + dr;
+      if (r0 + row >= a.N) row = a.N - 1 - r0;
+      woff[q] = uint32_t((row * a.K + int64_t(cs ^ (2 * q + dr)) * 8) * 2);
+    }
+  };
+  auto dma = [&](int64_t c, uint4 (*stage)[kMfmaSlices][kWave]) {
+    const uint32_t k0b = uint32_t(c * kMfmaKC * 2);
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int q = 0; q < (R2 && t ? R2 / 2 : kMfmaSlices); ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(t ? wres1 : wres0, (__attribute__((address_space(3))) void*)(&stage[t][q][0]),
+                                                 16, woff[q], k0b, 0, 2);
+  };
+
+  // The wave's chunks cb .. cb + CPW - 1 (the host checks K = NW * CPW * 256).
+  // The stationary X (and with NORM the norm weights, 16 bytes per thread
+  // for LDS) are requested first, then the ring's first two DMAs.  LDS is
+  // accessed through asm here: the compiler would make any LDS access
+  // behind the DMAs wait for all of them.
+  const int64_t cb = int64_t(wave) * CPW;
+  u32x4v_t xs[CPW][kMfmaSteps];
+  uint4 wv[NORM ? kNormW : 1];
+  if constexpr (NORM) {
+    // Rows past M read row 0: their outputs are never stored.
+    const uint16_t* xrow = a.X + (m < a.M ? m : 0) * a.ldx;
+#pragma unroll
+    for (int cc = 0; cc < CPW; ++cc)
+#pragma unroll
+      for (int s2 = 0; s2 < kMfmaSteps; ++s2)
+        xs[cc][s2] = *reinterpret_cast<const u32x4v_t*>(xrow + (cb + cc) * kMfmaKC + 32 * s2 + 8 * g);
+#pragma unroll
+    for (int j = 0; j < kNormW; ++j)
+      wv[j] = a.norm_w ? reinterpret_cast<const uint4*>(a.norm_w)[threadIdx.x + NW * kWave * j]
+                       : make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
+  } else {
+    const uint16_t* xpk = a.X + int64_t(blockIdx.y) * (a.K >> 5) * 512 + lane * 8;
+#pragma unroll
+    for (int cc = 0; cc < CPW; ++cc)
+#pragma unroll
+      for (int s2 = 0; s2 < kMfmaSteps; ++s2)
+        xs[cc][s2] = *reinterpret_cast<const u32x4v_t*>(xpk + ((cb + cc) * kMfmaSteps + s2) * 512);
+  }
+  set_rows(row0);
+  dma(cb, Wl0[wave]);
+  dma(cb + 1, Wl1[wave]);
+
+  float rs = 1.f;
+  const uint32_t wl_base = uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint4*)&wl[0]));
+  if constexpr (NORM) {
+#pragma unroll
+    for (int j = 0; j < kNormW; ++j)
+      asm volatile("ds_write_b128 %0, %1" ::"v"(wl_base + (threadIdx.x + NW * kWave * j) * 16u),
+                   "v"(__builtin_bit_cast(u32x4v_t, wv[j])));
+    // sum of squares of the lane's elements (row i), then the four lanes of
+    // row i (i, i + 16, i + 32, i + 48), then the four waves through LDS
+    float ss = 0.f;
+#pragma unroll
+    for (int cc = 0; cc < CPW; ++cc)
+#pragma unroll
+      for (int s2 = 0; s2 < kMfmaSteps; ++s2) {
+        float f[8];
+        unpack8(__builtin_bit_cast(uint4, xs[cc][s2]), f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
+      }
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+    ss = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+    ss = __uint_as_float(q[0]) + __uint_as_float(q[1]);
+    const uint32_t na = uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) float*)&nst[i][0]));
+    if (g == 0) asm volatile("ds_write_b32 %0, %1" ::"v"(na + wave * 4u), "v"(ss));
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    f32x4_t parts;
+    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(parts) : "v"(na));
+    rs = rsqrtf(((parts[0] + parts[1]) + (parts[2] + parts[3])) / float(a.K) + a.eps);
+  }
+  // Chunk cc of the stationary X normalised in place just before its first
+  // use (the ring streams on meanwhile; normalising every chunk up front,
+  // under the first two DMAs, measured slower: gate/up 36.1 -> 37.6 us).
+  auto normalise = [&](int cc) {
+    uint32_t addr[kMfmaSteps];
+#pragma unroll
+    for (int s2 = 0; s2 < kMfmaSteps; ++s2)
+      addr[s2] = wl_base + uint32_t(((cb + cc) * kMfmaKC + 32 * s2 + 8 * g) * 2);
+    u32x4v_t wf[kMfmaSteps];
+    lds_read_a8(addr, wf);
+#pragma unroll
+    for (int s2 = 0; s2 < kMfmaSteps; ++s2) {
+      float f[8], w[8];
+      unpack8(__builtin_bit_cast(uint4, xs[cc][s2]), f);
+      unpack8(__builtin_bit_cast(uint4, wf[s2]), w);
+      xs[cc][s2] = u32x4v_t{cvt_bf2(f[0] * rs * w[0], f[1] * rs * w[1]), cvt_bf2(f[2] * rs * w[2], f[3] * rs * w[3]),
+                            cvt_bf2(f[4] * rs * w[4], f[5] * rs * w[5]), cvt_bf2(f[6] * rs * w[6], f[7] * rs * w[7])};
+    }
+  };
+
+  f32x4_t acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](const uint4 (*stage)[kMfmaSlices][kWave], const u32x4v_t* x) {
+    u32x4v_t af[T][kMfmaSteps];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      uint32_t addr[kMfmaSteps];
+#pragma unroll
+      for (int s2 = 0; s2 < kMfmaSteps; ++s2)
+        addr[s2] = uint32_t(reinterpret_cast<uintptr_t>(
+            (__attribute__((address_space(3))) const uint4*)(&stage[t][i >> 1][(i & 1) * 32 + ((4 * s2 + g) ^ i)])));
+      lds_read_a8(addr, af[t]);
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < kMfmaSteps; ++s2)
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, af[t][s2]),
+                                                         __builtin_bit_cast(bf16x8_t, x[s2]), acc[t], 0, 0, 0);
+  };
+  auto epilogue = [&](int64_t r0) {
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) red[wave][t][j][lane] = acc[t][j];
+    __syncthreads();
+    const int j = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int64_t mo = m0 + (l & 15);
+    const int64_t n = r0 + 4 * (l >> 4) + j;
+    if (mo < a.M && n < a.N) {
+      float v[T];
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        float sacc = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) sacc += red[w][t][j][l];
+        v[t] = sacc;
+      }
+      if constexpr (R2 > 0) {
+        store_out(a, mo, n, v[0], 0.f);
+        if (4 * (l >> 4) + j < R2 && n + 16 < a.N) store_out(a, mo, n + 16, v[1], 0.f);
+      } else {
+        store_out(a, mo, n, v[0], SILU ? v[1] : 0.f);
+      }
+    }
+  };
+
+  int64_t rn = row0;  // rows of the tile the next DMA belongs to
+#pragma unroll
+  for (int idx = 0; idx < NC; ++idx) {
+    // outstanding once chunk idx has landed: chunk idx + 1's DMA
+    if (idx + 1 < NC) wait_vm<DN>(); else wait_vm<0>();
+    const int cc = idx % CPW;
+    auto* stage = (idx & 1) ? Wl1[wave] : Wl0[wave];
+    if constexpr (NORM) {
+      if (idx < CPW) normalise(cc);
+    }
+    compute(stage, xs[cc]);
+    if (idx + 2 < NC) {
+      const int64_t r = row0 + int64_t((idx + 2) / CPW) * stride;
+      if (r != rn) {
+        rn = r;
+        set_rows(r);
+      }
+      dma(cb + (idx + 2) % CPW, stage);
+    }
+    if (cc == CPW - 1) {  // tile done: reduce across waves and store
+      epilogue(row0 + int64_t(idx / CPW) * stride);
+#pragma unroll
+      for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      if (idx + 1 < NC) __syncthreads();  // red is rewritten by the next tile
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Row-block GEMV, M <= 4 and K % 8 == 0, K <= 16384.  A block of 256
 // threads is split into 256 / TPR row groups of TPR threads; each group owns
 // RB output rows (SwiGLU: RB gate rows and the RB matching up rows).  Thread
@@ -827,6 +1056,34 @@ void launch_mfma(const LinearArgs& a, hipStream_t s) {
   }
 }
 
+// The batched stages with the RMSNorm prologue (M > 4, K = 4096: four
+// 256-wide chunks per wave) run the X-stationary kernel, which normalises in
+// its prologue: gate/up with 2 or 3 tiles per CU as multi-tile blocks, the
+// 24-row blocks of a QKV-sized projection, and up to one 16-row tile per CU.
+// Larger shapes (an LM head) keep the staging pass and the streaming blocks.
+bool launch_xs_norm(const LinearArgs& a, hipStream_t s) {
+  if (a.K != 4 * 4 * kMfmaKC || a.x_packed) return false;
+  const int64_t cus = num_cus(), tx = (a.N + 15) / 16;
+  const unsigned gy = unsigned((a.M + 15) / 16);
+  const dim3 block(4 * kWave);
+  if (a.epi == kEpiSilu) {
+    if (tx == 3 * cus) hipLaunchKernelGGL((linear_xs_kernel<2, true, 4, 3, 0, true>), dim3(unsigned(cus), gy), block, 0, s, a);
+    else if (tx == 2 * cus) hipLaunchKernelGGL((linear_xs_kernel<2, true, 4, 2, 0, true>), dim3(unsigned(cus), gy), block, 0, s, a);
+    else if (tx * gy <= cus) hipLaunchKernelGGL((linear_xs_kernel<2, true, 4, 1, 0, true>), dim3(unsigned(tx), gy), block, 0, s, a);
+    else return false;
+    return true;
+  }
+  if (a.M <= 16 && a.N > 16 * cus && a.N <= 24 * cus) {
+    hipLaunchKernelGGL((linear_xs_kernel<2, false, 4, 1, 8, true>), dim3(unsigned((a.N + 23) / 24)), block, 0, s, a);
+    return true;
+  }
+  if (tx * gy <= cus) {
+    hipLaunchKernelGGL((linear_xs_kernel<1, false, 4, 1, 0, true>), dim3(unsigned(tx), gy), block, 0, s, a);
+    return true;
+  }
+  return false;
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
@@ -856,11 +1113,15 @@ int launch_linear(const LinearArgs& a, hipStream_t s) {
       silu ? launch_valu_m<false, true>(a, s) : launch_valu_m<false, false>(a, s);
     }
   } else {
-    // M > 4: the RMSNorm'd input is staged once as bf16(x * rsqrt(mean x^2 +
-    // eps) * w) (the reference's staging) into the caller's workspace, then
-    // a plain MFMA GEMM runs on it.  (Normalising inside the GEMM repeats the
-    // work in every block of 16 weight rows: measured slower than staging.)
+    // M > 4 with the RMSNorm prologue: the X-stationary kernel normalises in
+    // its prologue where the shape allows (one block per CU: every block
+    // loads X once anyway); otherwise the input is staged once as
+    // bf16(x * rsqrt(mean x^2 + eps) * w) (the reference's staging) into the
+    // caller's workspace and a plain MFMA GEMM runs on it (normalising inside
+    // the per-tile kernel repeats the work in every block of 16 weight rows:
+    // measured slower than staging).
     LinearArgs b = a;
+    if (a.norm && launch_xs_norm(a, s)) return launch_status("linear");
     if (a.norm) {
       EZ_REQUIRE(a.xn_ws, "linear: RMSNorm prologue with M > 4 needs a workspace (ezops_linear_stage_workspace_size)");
       EZ_REQUIRE(!a.x_packed && a.ldx == a.K, "linear: RMSNorm prologue with M > 4 needs contiguous X rows");

@@ -118,8 +118,8 @@ int launch_prefill_attn(const PrefillAttnArgs& a, hipStream_t s);
 int launch_silu_mul(const uint16_t* gu, uint16_t* out, int64_t T, int64_t IS, hipStream_t s);
 
 // Own MFMA GEMM (gemm.hip): Y[M,N] = X[M,K] W[N,K]^T, or bf16(R + bf16(X W^T))
-// with R (same layout as Y, may be Y); needs K % 64 == 0, ldx % 8 == 0 and
-// 16-byte aligned X and W.
+// with R (same layout as Y, may be Y); needs K % 8 == 0, ldx % 8 == 0,
+// ldx >= K, ldy >= N and 16-byte aligned X and W.
 bool gemm_mfma_supported(const uint16_t* X, int64_t ldx, const uint16_t* W, const uint16_t* Y, int64_t ldy,
                          const uint16_t* R, int64_t M, int64_t N, int64_t K);
 int gemm_mfma(const uint16_t* X, int64_t ldx, const uint16_t* W, uint16_t* Y, int64_t ldy, const uint16_t* R,
@@ -130,11 +130,9 @@ bool gemm_swiglu_supported(const uint16_t* X, int64_t ldx, const uint16_t* W, co
                            int64_t M, int64_t IS, int64_t K);
 int gemm_swiglu(const uint16_t* X, int64_t ldx, const uint16_t* W, uint16_t* Y, int64_t ldy, int64_t M, int64_t IS,
                 int64_t K, hipStream_t s);
-
-// Library GEMM (hipBLASLt): Y[M,N] = X[M,K] W[N,K]^T (+ R, same layout as Y).
-constexpr size_t kGemmWorkspace = size_t(32) << 20;
+// Any shape: the MFMA kernel where supported, else the linear-layer kernels.
 int gemm_bf16(const uint16_t* X, int64_t ldx, const uint16_t* W, uint16_t* Y, int64_t ldy, const uint16_t* R,
-              int64_t M, int64_t N, int64_t K, void* ws, size_t ws_bytes, hipStream_t s);
+              int64_t M, int64_t N, int64_t K, hipStream_t s);
 
 
 }  // namespace ez

@@ -69,8 +69,17 @@ def test_new_entry_points_reject_bad_arguments():
     # prefill attention: cache offsets are 32-bit, so S < 2^23 rows
     rc = lib.ezops_prefill_attn_bf16(d, d, d, d, d, None, 1, 16, 8, 8, 1 << 23, 128, 16, None, 0, 0, 0.0, None)
     assert rc == _hip.EINVAL and b"2^23" in lib.ezops_hip_last_error()
-    # library GEMM: empty shapes
-    assert lib.ezops_gemm_bf16(d, 16, d, d, 16, None, 0, 16, 16, d, 1 << 20, None) == _hip.EINVAL
+    # prefill GEMM: empty shapes, null operands, leading dimensions below the row length
+    assert lib.ezops_gemm_bf16(d, 16, d, d, 16, None, 0, 16, 16, None, 0, None) == _hip.EINVAL
+    assert lib.ezops_gemm_bf16(None, 16, d, d, 16, None, 4, 16, 16, None, 0, None) == _hip.EINVAL
+    assert lib.ezops_gemm_bf16(d, 8, d, d, 16, None, 4, 16, 16, None, 0, None) == _hip.EINVAL
+    assert lib.ezops_gemm_workspace_size() == 0
+    # fused gate/up + SwiGLU GEMM: null X / W / Y, ldx < K, IS < 1 (addresses 16-byte aligned)
+    a = 4096
+    for args in [(None, 64, a, a, 128, 16, 128, 64), (a, 64, None, a, 128, 16, 128, 64),
+                 (a, 64, a, None, 128, 16, 128, 64), (a, 32, a, a, 128, 16, 128, 64),
+                 (a, 64, a, a, 128, 16, 0, 64), (a, 64, a, a, 128, 16, 128, 0)]:
+        assert lib.ezops_gemm_swiglu_bf16(*args, None) == _hip.EINVAL, args
     # layer prefill: cu_seqlens is required
     p = _hip.Qwen3LayerParams(B=1, S=128, HS=256, IS=512, H=4, Hkv=2, D=128, hidden=d, K_cache=d, V_cache=d,
                               Wqkv=d, Wo=d, Wgu=d, Wd=d, out=d)

@@ -472,3 +472,30 @@ def test_linear_stage_streaming_blocks(M, extra, epi):
             np.testing.assert_allclose(n(Y), ref, rtol=1e-3, atol=1e-3)
         else:
             np.testing.assert_allclose(n(Y), ref, **BF_TOL)
+
+
+@pytest.mark.parametrize("M", [5, 16, 20])
+@pytest.mark.parametrize("shape", ["gate_up3", "gate_up2", "qkv24", "tiles"])
+def test_linear_stage_norm_in_kernel(M, shape):
+    """Batched stages with the RMSNorm prologue at K = 4096 normalise inside
+    the X-stationary kernel (no staging pass): gate/up with 3 and 2 tiles per
+    CU (multi-tile blocks), the 24-row QKV blocks, and a few 16-row tiles;
+    M = 20 spans two batch blocks (multi-tile and one-tile shapes)."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    K = 4096
+    N, epi = {"gate_up3": (48 * cus, 2), "gate_up2": (32 * cus, 2), "qkv24": (24 * cus, 0), "tiles": (200, 1)}[shape]
+    if shape == "qkv24" and M > 16:
+        N = 16 * cus // 2  # M > 16 has no 24-row blocks; one tile per CU at most
+    rng = np.random.default_rng(M + N)
+    X = oracle.bf16(rng.standard_normal((M, K)).astype(np.float32) * 2)
+    W = oracle.bf16(rng.standard_normal((N, K)).astype(np.float32) * K ** -0.5)
+    W2 = oracle.bf16(rng.standard_normal((N, K)).astype(np.float32) * K ** -0.5)
+    R = oracle.bf16(rng.standard_normal((M, N)).astype(np.float32))
+    w = oracle.bf16(rng.standard_normal(K).astype(np.float32) * 0.1 + 1)
+    ref = _stage_ref(X, W, W2, R, w, 1, epi)
+    tX, tW, tW2, tR, tw = g(X), g(W), g(W2), g(R), g(w)
+    Y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=DEV)
+    ws = torch.zeros(_hip.size("ezops_linear_stage_workspace_size", M, K, 1), dtype=torch.uint8, device=DEV)
+    _hip.call("ezops_linear_stage_bf16", tX.data_ptr(), K, tW.data_ptr(), tW2.data_ptr(), Y.data_ptr(), N,
+              tR.data_ptr(), N, tw.data_ptr(), 1, 1e-6, epi, M, N, K, ws.data_ptr(), ws.numel(), _hip.stream())
+    np.testing.assert_allclose(n(Y), ref, **BF_TOL)

@@ -92,7 +92,9 @@ QWEN3_8B = dict(hidden_size=4096, intermediate_size=12288, num_heads=32, head_di
 @pytest.mark.parametrize("M,N,K,resid", [
     (512, 6144, 4096, False), (77, 4096, 12288, True), (1, 200, 64, True),  # the MFMA kernel
     (300, 520, 128, False), (256, 256, 64, True), (4096, 768, 4096, "alias"),  # tile tails, one tile, R = Y
-    (33, 100, 100, False), (5, 64, 72, True),  # K % 64 != 0: the hipBLASLt fallback
+    (33, 100, 72, False), (5, 64, 72, True), (300, 520, 1000, "alias"), (257, 4100, 4104, True),
+    (1024, 1024, 3000, False),  # K % 64 != 0: the MFMA kernel's masked last K-step
+    (33, 100, 100, False), (70, 40, 9, True),  # K % 8 != 0: the linear-layer kernels
 ])
 def test_gemm_vs_oracle(M, N, K, resid):
     rng = np.random.default_rng(M + N)
@@ -177,7 +179,8 @@ def test_gemm_swiglu_full_and_partial_grid_bit_identical():
     torch.testing.assert_close(out[M][:512].float(), ref, rtol=2e-2, atol=2e-2)
 
 
-@pytest.mark.parametrize("M,IS,K", [(300, 384, 256), (512, 1024, 512), (257, 128, 64)])
+@pytest.mark.parametrize("M,IS,K", [(300, 384, 256), (512, 1024, 512), (257, 128, 64), (300, 384, 200),
+                                    (129, 256, 1096)])
 def test_gemm_swiglu_vs_unfused(M, IS, K):
     """The fused gate/up + SwiGLU GEMM against the plain GEMM into [M, 2 IS]
     followed by SwiGLU on the host (bf16 gate/up, bf16 activation, bf16
