@@ -189,13 +189,24 @@ def prefill(torch, flush) -> dict:
 
 
 def cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it (model name, family / model /
+    stepping, clock) and the logical CPUs this process may run on."""
+    info = {}
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                k, v = (t.strip() for t in line.split(":", 1))
+                info.setdefault(k, v)
     except OSError:
         pass
-    return platform.processor() or platform.machine()
+    name = info.get("model name") or platform.processor() or platform.machine()
+    fms = "/".join(info.get(k, "?") for k in ("cpu family", "model", "stepping"))
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count() or 1
+    mhz = f", {float(info['cpu MHz']):.0f} MHz" if "cpu MHz" in info else ""
+    return f"{name} (family/model/stepping {fms}{mhz}; {avail} logical CPUs available to the process)"
 
 
 def cpu_ref_baseline(torch, layer_data, lens, budget_s: float = 4.0) -> dict:
@@ -204,13 +215,16 @@ def cpu_ref_baseline(torch, layer_data, lens, budget_s: float = 4.0) -> dict:
     all host threads, 2 warm-ups then the median of >= 5 timed runs per op.
 
     Inputs are this run's GPU tensors copied to the host, so both sides see the
-    same values.  Per op: G, N (RMSNorm / softmax / sum), A (a sample of 4 of
-    the 32 sequences, scaled x8 to the full config), F1 and F2 at batch 1, and
-    the config-L layer at the headline batch."""
+    same values.  Per op, each at its configuration's full size: G, N
+    (RMSNorm / softmax / sum), A (all 32 sequences), F1 and F2 at batch 1,
+    and the config-L layer at the headline batch."""
     from ezops import (AttnDecodeOp, FusedOProjFfnOp, FusedQkNormRopeOp, GemvOp, Qwen3DenseDecodeOp, ReduceOp,
                        RmsNormOp, SoftmaxOp, workloads)
 
-    threads = os.cpu_count() or 1
+    try:
+        threads = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     cpu = lambda ts: [t.cpu() for t in ts]  # noqa: E731
 
@@ -253,11 +267,9 @@ def cpu_ref_baseline(torch, layer_data, lens, budget_s: float = 4.0) -> dict:
     rec("sum_f32_2^28", lambda: rd(A, Ao), 1_073_741_828)
     del A, nd
     torch.cuda.empty_cache()
-    Q, K, V = workloads.config_a("cuda")
-    Q, K, V = Q[:4].cpu(), K[:4].cpu(), V[:4].cpu()
-    at = AttnDecodeOp(4, 32, 8192, 128, num_kv_heads=8)
-    rec("gqa_decode_b32_h32_kv8_s8192", lambda: at(Q, K, V), 1_074_266_112, scale=8,
-        sample="4 of the 32 sequences timed, x8")
+    Q, K, V = cpu(workloads.config_a("cuda"))
+    at = AttnDecodeOp(32, 32, 8192, 128, num_kv_heads=8)
+    rec("gqa_decode_b32_h32_kv8_s8192", lambda: at(Q, K, V), 1_074_266_112)
     del Q, K, V
     torch.cuda.empty_cache()
     pos, *f1 = workloads.config_f1(1, "cuda")
@@ -371,6 +383,14 @@ def op_table(torch, _hip, flush) -> dict:
     return out
 
 
+# (N, K) of the batch-1 GEMVs profiled cold: the reference's GEMV bench shape
+# (benchmarks/bench_gemv.py:26-33), then the Qwen3-0.6B and Qwen3-VL-2B
+# projections (QKV, o_proj, gate/up as one 2 IS-row matrix, down).
+GEMV_SHAPES = [(4096, 2048),
+               (4096, 1024), (1024, 2048), (6144, 1024), (1024, 3072),
+               (4096, 2048), (2048, 2048), (12288, 2048), (2048, 6144)]
+
+
 def profile_only(torch, _hip, flush, args) -> int:
     """Launch one kernel 10 times (each after a read flush) so a profiler can count its traffic.
 
@@ -385,6 +405,11 @@ def profile_only(torch, _hip, flush, args) -> int:
              streaming-read probes (the looping one, then the one-shot-block
              one) over 50.3, 38.05, 33.57, 201.4 and 100.7 MB (QKV, attention
              K/V, o_proj, gate/up, down), 10 cold dispatches each, in that order.
+    gemv_shapes: batch-1 GEMVs at the reference's bench shape and the
+             Qwen3-0.6B / VL-2B projection shapes (GEMV_SHAPES, in order), 10
+             cold dispatches each, then the two streaming-read probes (looping,
+             then one-shot blocks) over each shape's weight bytes, 10 cold
+             dispatches each.
     """
     if args.profile_kernel in ("gemv", "attn_a"):
         from ezops import AttnDecodeOp, GemvOp, workloads
@@ -401,6 +426,26 @@ def profile_only(torch, _hip, flush, args) -> int:
         for _ in range(10):
             flush()
             fn()
+    elif args.profile_kernel == "gemv_shapes":
+        from ezops import GemvOp
+
+        for N, K in GEMV_SHAPES:
+            x = torch.randn(K, device="cuda").to(torch.bfloat16)
+            W = (torch.randn(N, K, device="cuda") * 0.02).to(torch.bfloat16)
+            y = torch.empty(N, dtype=torch.bfloat16, device="cuda")
+            g = GemvOp(N, K, backend="hip")
+            for _ in range(10):
+                flush()
+                g(x, W, y)
+            del x, W, y
+        buf = torch.zeros(max(N * K for N, K in GEMV_SHAPES) // 2 + 16, device="cuda")
+        sink = torch.zeros(16, device="cuda")
+        for kind in (4, 5):
+            for N, K in GEMV_SHAPES:
+                for _ in range(10):
+                    flush()
+                    _hip.call("ezops_hbm_probe", kind, sink.data_ptr(), buf.data_ptr(), None, N * K // 2, 0.0,
+                              _hip.stream())
     elif args.profile_kernel == "prefill":
         from ezops import Qwen3PrefillOp
 
@@ -455,7 +500,7 @@ def main() -> int:
     ap.add_argument("--no-step", action="store_true", help="skip the 36-layer decode-step timing")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill timings")
     ap.add_argument("--batch", type=int, default=1, help="layer batch (headline is 1)")
-    ap.add_argument("--profile-kernel", choices=["gate_up", "copy", "layer", "prefill", "gemv", "attn_a", "burst"],
+    ap.add_argument("--profile-kernel", choices=["gate_up", "copy", "layer", "prefill", "gemv", "attn_a", "burst", "gemv_shapes"],
                     help="only launch this kernel 10x between read flushes (for rocprofv3 counter runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

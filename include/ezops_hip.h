@@ -275,10 +275,8 @@ int ezops_qwen3_decode_step_bf16(const ezops_qwen3_layer* layers, int64_t n_laye
  * p->max_kv_len is unused.  block_table != NULL: paged caches as in
  * ezops_qwen3_dense_decode_paged_bf16.  max_q_len: host bound on the
  * per-sequence token counts.  D = 128, IS % 8 == 0.  The projections run
- * the library's MFMA GEMM (see ezops_gemm_bf16) when HS, IS and H*D are
- * multiples of 64 (deterministic, allocation-free); other shapes use
- * hipBLASLt, whose first call of a shape sets up and times its algorithm on
- * the host (run such shapes eagerly once before capturing a graph).
+ * the library's own GEMM (see ezops_gemm_bf16): deterministic,
+ * allocation-free and graph-capturable for every shape.
  * No counterpart in the reference (decode only,
  * ezops/ops/qwen3_dense_decode.py:9-176): the step that fills the cache the
  * decode layer reads. */
@@ -290,10 +288,11 @@ int ezops_qwen3_prefill_bf16(const ezops_qwen3_layer* p, int64_t T, const int32_
 
 /* GEMM used by prefill: Y[M, N] = X[M, K] W[N, K]^T, and with R != NULL
  * (R [M, N], same leading dimension as Y; may be Y) Y = bf16(R + bf16(X W^T));
- * bf16 in/out, fp32 accumulation.  K % 64 == 0 with ldx % 8 == 0 and 16-byte
- * aligned X and W runs the library's own MFMA kernel (no workspace used);
- * other shapes fall back to hipBLASLt (the residual then rounds once:
- * bf16(R + X W^T)).  workspace: ezops_gemm_workspace_size() bytes.
+ * bf16 in/out, fp32 accumulation.  K % 8 == 0 with ldx % 8 == 0 and 16-byte
+ * aligned X and W runs the MFMA kernel (a partial last K-step is masked);
+ * other shapes run the library's linear-layer kernels, with the same
+ * rounding.  No workspace is used: ezops_gemm_workspace_size() returns 0
+ * and `workspace` may be NULL (kept for the ABI).
  * No counterpart in the reference (its GEMMs are decode GEMVs). */
 size_t ezops_gemm_workspace_size(void);
 int ezops_gemm_bf16(const void* X, int64_t ldx, const void* W, void* Y, int64_t ldy, const void* R,
@@ -304,8 +303,8 @@ int ezops_gemm_bf16(const void* X, int64_t ldx, const void* W, void* Y, int64_t 
  * Y[M, IS] = bf16(bf16(silu(bf16(X Wg^T))) * bf16(X Wu^T)) with Wgu = [Wg; Wu]
  * as [2 IS, K] (the layer's gate/up weight), bit-identical to
  * ezops_gemm_bf16 into [M, 2 IS] followed by the SwiGLU pass.  Requires
- * IS % 128 == 0, K % 64 == 0, ldx % 8 == 0, ldy % 8 == 0, ldy >= IS and
- * 16-byte aligned X, Wgu, Y (EZOPS_EINVAL otherwise).
+ * IS % 128 == 0, K % 8 == 0, ldx >= K, ldx % 8 == 0, ldy % 8 == 0, ldy >= IS
+ * and non-null, 16-byte aligned X, Wgu, Y (EZOPS_EINVAL otherwise).
  * No counterpart in the reference (its FFN is the decode GEMV chain). */
 int ezops_gemm_swiglu_bf16(const void* X, int64_t ldx, const void* Wgu, void* Y, int64_t ldy, int64_t M,
                            int64_t IS, int64_t K, hipStream_t stream);
