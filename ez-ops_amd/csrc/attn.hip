@@ -190,6 +190,25 @@ __device__ __forceinline__ RopeIn load_rope(const uint16_t* crow, const uint16_t
   const int l = lane & (D / 2 - 1);
   return RopeIn{crow[l], crow[l + D / 2], srow[l], srow[l + D / 2]};
 }
+// load_rope for a position known only after the tile loads went out: the
+// loads and their wait in one asm block, so that the speculative rows'
+// registers (requested before the tiles) are all that the merge of the two
+// paths waits for.
+template <int D>
+__device__ __forceinline__ RopeIn load_rope_sync(const uint16_t* crow, const uint16_t* srow, int lane) {
+  const int l = lane & (D / 2 - 1);
+  uint32_t c1, c2, s1, s2;
+  asm volatile(
+      "global_load_ushort %0, %4, off\n\t"
+      "global_load_ushort %1, %5, off\n\t"
+      "global_load_ushort %2, %6, off\n\t"
+      "global_load_ushort %3, %7, off\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(c1), "=&v"(c2), "=&v"(s1), "=&v"(s2)
+      : "v"(crow + l), "v"(crow + l + D / 2), "v"(srow + l), "v"(srow + l + D / 2)
+      : "memory");
+  return RopeIn{uint16_t(c1), uint16_t(c2), uint16_t(s1), uint16_t(s2)};
+}
 template <int D>
 __device__ __forceinline__ void finish_head(const HeadIn& in, const RopeIn& ro, bool weighted, bool rope, float eps,
                                             uint16_t* dst, int lane) {
@@ -295,8 +314,14 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
   }
   // The length is requested first, ahead of this wave's tile loads, and
   // unconditionally (a dummy address without kv_lens), so that nothing waits
-  // for it before its first use.
-  const int32_t Lraw = *(a.kv_lens ? a.kv_lens + b : reinterpret_cast<const int32_t*>(a.K));
+  // for it before its first use.  It is a vector load (an opaque per-lane
+  // zero in the address): a wave's vector loads complete in order, so the
+  // first one returns first, whereas a scalar load issued beside the tile
+  // flood waited 3.5-10 us for its cache line (per-wave stamps, B = 1).
+  int32_t lane0;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(lane0));
+  const int32_t Lv = (a.kv_lens ? a.kv_lens + b : reinterpret_cast<const int32_t*>(a.K))[lane0];
+  __builtin_amdgcn_sched_barrier(0);
   KvRows<D, PAGED> kr{}, vr{};
   if constexpr (PAGED) {
     const int32_t* bt = a.block_table + int64_t(b) * a.bt_stride;
@@ -311,10 +336,15 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
   }
   const int64_t h0 = int64_t(kvh) * G;  // first query head of the group
   const float sl2 = a.scale * kLog2e;
-  const int64_t stride = int64_t(nsb) * W * kTile;  // distance between a wave's tiles
+  // Tiles of this wave: interleaved over the splits (tile s W + w, then every
+  // nsb W-th), or with a.tps > 0 the split's own contiguous range (tile
+  // s tps + w, then every W-th, below t_end) -- every block then carries the
+  // same bytes, which sets the time when there is one block per CU.
+  const int64_t stride = (a.tps > 0 ? int64_t(1) : int64_t(nsb)) * W * kTile;  // distance between a wave's tiles
+  const int64_t t_end = a.tps > 0 ? min(a.Lh, (int64_t(split) + 1) * a.tps * kTile) : a.Lh;
   uint16_t* slab = &Vs[wave][0];
 
-  int64_t t0 = (int64_t(split) * W + wave) * kTile;
+  int64_t t0 = (a.tps > 0 ? int64_t(split) * a.tps + wave : int64_t(split) * W + wave) * kTile;
   uint4 kn[VI], vn[VI];
 
   // Layer prologue inputs, requested ahead of the first tile and without
@@ -339,24 +369,30 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
     const uint16_t* vrow = row + (a.H + a.Hkv) * D + int64_t(kvh) * D;
     vv1 = vrow[lane & (D / 2 - 1)];
     vv2 = vrow[(lane & (D / 2 - 1)) + D / 2];
-    int64_t pos = int64_t(a.kv_lens ? Lraw : int32_t(a.S)) - 1;
-    pos = pos < 0 ? 0 : (pos >= a.Lh ? a.Lh - 1 : pos);  // the address only; L = 0 writes nothing
-    rin = load_rope<D>(a.cos ? a.cos + pos * D : row, a.sin ? a.sin + pos * D : row, lane);
+    // The rows of the host's bound Lh - 1, which is the token position
+    // whenever the sequence is the longest (B = 1 with an exact bound): no
+    // wait for the length before the tile loads go out.  Another position
+    // reloads them once the length is in (below).
+    const int64_t pos_s = a.Lh > 0 ? a.Lh - 1 : 0;
+    rin = load_rope<D>(a.cos ? a.cos + pos_s * D : row, a.sin ? a.sin + pos_s * D : row, lane);
   }
   __builtin_amdgcn_sched_barrier(0);
   {
-    const int64_t ts = tile_start(t0, a.Lh - 1);
+    const int64_t ts = tile_start(t0, t_end - 1);
     const int32_t id = kr.page_id(ts, lane);
-    load_k_regs<D>(kr.at(ts, id), ts, t0, a.Lh - 1, lane, kn);
-    load_v_regs<D>(vr.at(ts, id), ts, t0, a.Lh - 1, lane, vn);
+    load_k_regs<D>(kr.at(ts, id), ts, t0, t_end - 1, lane, kn);
+    load_v_regs<D>(vr.at(ts, id), ts, t0, t_end - 1, lane, vn);
   }
   __builtin_amdgcn_sched_barrier(0);
 
+  int32_t Lraw;  // read here, behind the tile loads (asm: not hoisted to the load)
+  asm volatile("v_readfirstlane_b32 %0, %1" : "=s"(Lraw) : "v"(Lv));
   int64_t L = a.kv_lens ? int64_t(Lraw) : a.S;
   L = L < 0 ? 0 : (L > a.Lh ? a.Lh : L);
   // Cache rows read here: [0, Lc) (the layer's decoded token is the virtual row).
   const int64_t Lc = LAYER ? (L > 0 ? L - 1 : 0) : L;
-  const int64_t cl = Lc > 0 ? Lc - 1 : 0;  // clamp row of later tiles
+  const int64_t Le = Lc < t_end ? Lc : t_end;  // this wave's tiles lie below Le
+  const int64_t cl = Le > 0 ? Le - 1 : 0;      // clamp row of later tiles
   // Paged: the table entry of the next tile is read one iteration ahead.
   int32_t id_next = kr.page_id(tile_start(t0 + stride, cl), lane);
 
@@ -365,6 +401,7 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
     const int64_t pos = L - 1;
     if (L > 0) {
       const bool rope = a.cos != nullptr;
+      if (rope && pos != (a.Lh > 0 ? a.Lh - 1 : 0)) rin = load_rope_sync<D>(a.cos + pos * D, a.sin + pos * D, lane);
 #pragma unroll
       for (int j = 0; j < NQ; ++j)
         if (wave + j * W < G) finish_head<D>(qin[j], rin, a.qw != nullptr, rope, a.eps, &Qs[wave + j * W][0], lane);
@@ -421,7 +458,7 @@ __global__ __launch_bounds__(W * kWave) void attn_split_kernel(AttnArgs a, int n
 #pragma unroll
   for (int db = 0; db < NDB; ++db) o[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int it = 0; t0 < Lc; t0 += stride, ++it) {
+  for (int it = 0; t0 < Le; t0 += stride, ++it) {
     const int64_t tn = t0 + stride;
     // ---- S^T = K Q^T: acc[u][r] = S[head li][pos t0 + 16u + 4lg + r]
     // this tile's K from its registers into the slab (the previous tile's
@@ -703,9 +740,25 @@ int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
   aa.Lh = (a.Lh == 0 || a.Lh > a.S || !a.kv_lens) ? a.S : a.Lh;
   aa.sort_lens = a.kv_lens && a.B > 1 && a.B <= kWave;
   if (aa.scale <= 0.f) aa.scale = 1.0f / sqrtf(float(a.D));
-  const SplitPlan pl = plan_splits(aa.B, aa.Hkv, aa.Lh, G);
+  SplitPlan pl = plan_splits(aa.B, aa.Hkv, aa.Lh, G);
   // ragged batches: splits in proportion to each sequence's length
   aa.split_chunk = (aa.sort_lens && pl.nsplit > 1) ? (aa.Lh + pl.nsplit - 1) / pl.nsplit : 0;
+  aa.tps = 0;
+  if (!aa.split_chunk && pl.waves == 8) {
+    // Few units (8-wave blocks): one block per CU, each over its own
+    // contiguous run of tiles, so that every CU reads the same bytes (the
+    // interleaved plan put 16 tiles on some CUs and none on a third of
+    // them; a CU streams about 21 GB/s here, so the busiest CU sets the
+    // time).  nsplit is then the number of non-empty runs.
+    const int64_t tiles = (aa.Lh + kTile - 1) / kTile;
+    const int64_t ws_ns = plan_splits(a.B, a.Hkv, a.S, G, false).nsplit;  // what the workspace holds
+    int64_t ns = num_cus() / (aa.B * aa.Hkv);
+    ns = ns < ws_ns ? ns : ws_ns;
+    ns = ns < (tiles + 7) / 8 ? ns : (tiles + 7) / 8;  // at least a tile per wave
+    ns = ns < 1 ? 1 : ns;
+    aa.tps = (tiles + ns - 1) / ns;
+    pl.nsplit = int((tiles + aa.tps - 1) / aa.tps);
+  }
   float *opart = nullptr, *ml = nullptr;
   if (pl.nsplit > 1) {
     const size_t need = attn_workspace_size(a.B, a.H, a.Hkv, a.S, a.D);

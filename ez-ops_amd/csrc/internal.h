@@ -82,6 +82,7 @@ struct AttnArgs {
   int out_packed;     // Out in the MFMA-packed layout of [B, H*D] (the layer's o_proj input)
   int sort_lens;      // set by the launcher: serve the sequences longest first
   int64_t split_chunk;  // set by the launcher: > 0 = ragged batch, ceil(len / split_chunk) splits per sequence
+  int64_t tps;          // set by the launcher: > 0 = split s owns the contiguous tiles [s tps, (s + 1) tps)
   int64_t Lh;         // bound on the live lengths for planning (0 = S); lengths above it are cut to it
   float scale;
   // Fused layer prologue (Q == NULL): q/k/v of the decoded token come from
