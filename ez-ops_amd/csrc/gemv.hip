@@ -525,7 +525,7 @@ __global__ __launch_bounds__(4 * kWave) void linear_xs_kernel(LinearArgs a) {
   __shared__ __align__(16) uint4 Wl0[NW][T][kMfmaSlices][kWave];
   __shared__ __align__(16) uint4 Wl1[NW][T][kMfmaSlices][kWave];
   __shared__ float red[NW][T][4][kWave];
-  __shared__ float nst[16][NW];
+  __shared__ __align__(16) float nst[16][NW];  // read back a row at a time (ds_read_b128)
   __shared__ uint4 wl[NORM ? NW * CPW * kMfmaKC / 8 : 1];  // the norm weights (K bf16)
 
   const int lane = threadIdx.x & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -598,6 +598,10 @@ __global__ __launch_bounds__(4 * kWave) void linear_xs_kernel(LinearArgs a) {
   set_rows(row0);
   dma(cb, Wl0[wave]);
   dma(cb + 1, Wl1[wave]);
+  // every DMA goes out before anything waits for X (the scheduler would
+  // otherwise interleave the statistics with the DMA issue, which then
+  // waits behind the X loads and part of the first chunk)
+  __builtin_amdgcn_sched_barrier(0);
 
   float rs = 1.f;
   const uint32_t wl_base = uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint4*)&wl[0]));
