@@ -43,7 +43,7 @@ def _run(name, Q, K, V, lens, ws=None):
 def _reference(Q, K, V, lens):
     B, H, D = Q.shape
     nbytes = _hip.size("ezops_attn_decode_workspace_size", B, H, K.shape[1], K.shape[2], D)
-    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=DEV)
+    ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=DEV)  # zero-filled, as the ABI asks
     return _run("ezops_attn_decode_bf16", Q, K, V, lens, ws)
 
 
