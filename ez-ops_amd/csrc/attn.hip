@@ -744,12 +744,14 @@ int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
   // ragged batches: splits in proportion to each sequence's length
   aa.split_chunk = (aa.sort_lens && pl.nsplit > 1) ? (aa.Lh + pl.nsplit - 1) / pl.nsplit : 0;
   aa.tps = 0;
-  if (!aa.split_chunk && pl.waves == 8) {
+  if (!aa.split_chunk && pl.waves == 8 && (!a.kv_lens || a.Lh > 0)) {
     // Few units (8-wave blocks): one block per CU, each over its own
     // contiguous run of tiles, so that every CU reads the same bytes (the
     // interleaved plan put 16 tiles on some CUs and none on a third of
     // them; a CU streams about 21 GB/s here, so the busiest CU sets the
-    // time).  nsplit is then the number of non-empty runs.
+    // time).  nsplit is then the number of non-empty runs.  Only with a host
+    // bound on the lengths (or none to bound): over the capacity S with
+    // shorter lengths, the runs past them would leave their CUs idle.
     const int64_t tiles = (aa.Lh + kTile - 1) / kTile;
     const int64_t ws_ns = plan_splits(a.B, a.Hkv, a.S, G, false).nsplit;  // what the workspace holds
     int64_t ns = num_cus() / (aa.B * aa.Hkv);
