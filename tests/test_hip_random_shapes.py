@@ -88,3 +88,30 @@ def test_gemm_random(seed):
     if resid:
         ref = oracle.bf16(R + ref)
     np.testing.assert_allclose(n(Y), ref, **BF_TOL, err_msg=f"M={M} N={N} K={K} ldx={ldx} resid={resid}")
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_attn_decode_random(seed):
+    """Decode attention over random batch, group size, head_dim, capacity,
+    ragged lengths and length bound (none, exact, loose): the interleaved,
+    contiguous-run and ragged split plans."""
+    rng = np.random.default_rng(3000 + seed)
+    B = int(rng.integers(1, 9))
+    G = int(rng.choice([1, 2, 4, 8, 16]))
+    Hkv = int(rng.choice([1, 2, 8])) if G < 16 else 1
+    H, D = G * Hkv, int(rng.choice([64, 128]))
+    S = int(rng.integers(1, 3000))
+    lens = rng.integers(1, S + 1, size=B).astype(np.int32)
+    hint = int(rng.choice([0, lens.max(), min(S, lens.max() + 97)]))
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    Q = torch.randn(B, H, D, generator=gen, device=DEV).to(torch.bfloat16)
+    K = torch.randn(B, Hkv, S, D, generator=gen, device=DEV).to(torch.bfloat16)
+    V = torch.randn(B, Hkv, S, D, generator=gen, device=DEV).to(torch.bfloat16)
+    tl = torch.from_numpy(lens).to(DEV)
+    out = torch.full((B, H, D), float("nan"), dtype=torch.bfloat16, device=DEV)
+    ws = torch.zeros(max(256, _hip.size("ezops_attn_decode_workspace_size", B, H, Hkv, S, D)), dtype=torch.uint8,
+                     device=DEV)
+    _hip.call("ezops_attn_decode_bf16", Q.data_ptr(), K.data_ptr(), V.data_ptr(), out.data_ptr(), B, H, Hkv, S, D,
+              tl.data_ptr(), hint, 0.0, ws.data_ptr(), ws.numel(), _hip.stream())
+    ref = oracle.attn_decode(n(Q), n(K), n(V), kv_lens=lens)
+    np.testing.assert_allclose(n(out), ref, **BF_TOL, err_msg=f"B={B} H={H} Hkv={Hkv} S={S} D={D} hint={hint}")
