@@ -325,6 +325,14 @@ def op_table(torch, _hip, flush) -> dict:
     op = GemvOp(4096, 4096, backend="hip")
     rec("gemv_4096x4096", lambda i: op(x, Ws[i % 12], y), 33_570_816, 24, copies=12)
     del Ws
+    # The same op at a size where the launch ramp and tail are amortised
+    # (the Qwen3-8B LM head, 1.24 GB per launch > the MALL): the GEMV's
+    # sustained bandwidth, beside config G's 33.6 MB one-shot figure.
+    Wl = [randn(151936, 4096, std=0.02) for _ in range(2)]
+    yl = torch.empty(151936, dtype=torch.bfloat16, device="cuda")
+    opl = GemvOp(151936, 4096, backend="hip")
+    rec("gemv_151936x4096", lambda i: opl(x, Wl[i % 2], yl), 151936 * 4096 * 2 + 4096 * 2 + 151936 * 2, 4, copies=2)
+    del Wl
 
     gcu.manual_seed(1)
     Xs = [randn(64, 4096) for _ in range(8)]
@@ -399,7 +407,7 @@ def profile_only(torch, _hip, flush, args) -> int:
              calibration kernel for FETCH_SIZE / WRITE_SIZE.
     layer:   one full B=1 layer step.
     prefill: one Qwen3-8B layer prefill over a fresh 4096-token prompt.
-    gemv:    the config-G GEMV (4096 x 4096 bf16, 33,570,816 algorithmic bytes).
+    gemv:    the config-G GEMV (4096 x 4096 bf16, 33,570,816 algorithmic bytes), 30 dispatches.
     attn_a:  the config-A GQA decode (B=32, 32/8 heads, S=8192; 1,074,266,112 bytes).
     burst:   the one-shot read roofline of the B=1 layer's stages: the two
              streaming-read probes (the looping one, then the one-shot-block
@@ -423,7 +431,7 @@ def profile_only(torch, _hip, flush, args) -> int:
             Q, K, V = workloads.config_a("cuda")
             at = AttnDecodeOp(32, 32, 8192, 128, backend="hip", num_kv_heads=8)
             fn = lambda: at(Q, K, V)  # noqa: E731
-        for _ in range(10):
+        for _ in range(30 if args.profile_kernel == "gemv" else 10):
             flush()
             fn()
     elif args.profile_kernel == "gemv_shapes":
