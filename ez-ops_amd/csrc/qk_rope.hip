@@ -233,6 +233,7 @@ extern "C" int ezops_qk_norm_rope_bf16(const void* q, int64_t q_bs, const void* 
   a.position = position; a.positions = positions; a.pos_offset = pos_offset;
   a.eps = eps;
   EZ_REQUIRE(q_out, "qk_norm_rope: null pointer");
+  EZ_REQUIRE(H >= 1 && Hkv >= 1, "qk_norm_rope: num_heads and num_kv_heads must be >= 1");
   EZ_REQUIRE(H % Hkv == 0, "qk_norm_rope: num_heads must be divisible by num_kv_heads");
   EZ_REQUIRE(positions || (position + pos_offset >= 0 && position + pos_offset < S),
              "qk_norm_rope: position out of range");

@@ -91,6 +91,10 @@ def test_new_entry_points_reject_bad_arguments():
     rc = lib.ezops_qwen3_decode_step_bf16(layers, 2, None, 0, 0, None, None, 0, None, d, 1 << 20, None)
     assert rc == _hip.EINVAL and b"shape" in lib.ezops_hip_last_error()
     assert lib.ezops_qwen3_decode_step_bf16(layers, 0, None, 0, 0, None, None, 0, None, d, 1 << 20, None) == _hip.EINVAL
+    # QK-norm + RoPE: zero kv heads is rejected before the head-group division
+    rc = lib.ezops_qk_norm_rope_bf16(d, 128, d, 128, d, 128, None, None, None, None, d, d, d, d, 1, 4, 0, 128, 16, 0,
+                                     None, 0, 1e-6, None)
+    assert rc == _hip.EINVAL and b"num_kv_heads" in lib.ezops_hip_last_error()
     # a paged decode step needs page_size a power of two dividing S
     same = (_hip.Qwen3LayerParams * 1)()
     same[0] = _hip.Qwen3LayerParams(B=1, S=128, HS=256, IS=512, H=4, Hkv=2, D=128, hidden=d, out=d)
