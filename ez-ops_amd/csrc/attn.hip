@@ -721,7 +721,7 @@ size_t attn_workspace_size(int64_t B, int64_t H, int64_t Hkv, int64_t S, int64_t
   return align256(size_t(B * H * pl.nsplit * D) * 4) + align256(size_t(B * H * pl.nsplit * 2) * 4);
 }
 
-int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
+int check_attn(const AttnArgs& a) {
   const bool layer = a.Q == nullptr;
   EZ_REQUIRE(a.K && a.V && a.Out && (!layer || a.qkv), "attn_decode: null pointer");
   EZ_REQUIRE(a.B >= 1 && a.H >= 1 && a.Hkv >= 1 && a.S >= 1, "attn_decode: bad shape");
@@ -736,6 +736,14 @@ int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
   EZ_REQUIRE(!a.block_table || (a.page_size >= kTile && (a.page_size & (a.page_size - 1)) == 0 &&
                                 a.bt_stride >= 1 && a.S == a.bt_stride * a.page_size),
              "paged attn_decode: page_size must be a power of two >= %d and S = max_pages * page_size", kTile);
+  return EZ_OK;
+}
+
+int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
+  const int rc = check_attn(a);
+  if (rc != EZ_OK) return rc;
+  const bool layer = a.Q == nullptr;
+  const int64_t G = a.H / a.Hkv;
   AttnArgs aa = a;
   aa.Lh = (a.Lh == 0 || a.Lh > a.S || !a.kv_lens) ? a.S : a.Lh;
   aa.sort_lens = a.kv_lens && a.B > 1 && a.B <= kWave;

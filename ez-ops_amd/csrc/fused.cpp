@@ -138,9 +138,6 @@ int run_layer(const ezops_qwen3_layer* p, const int32_t* block_table, int64_t nu
   l.X = hidden; l.ldx = p->HS; l.W = static_cast<const uint16_t*>(p->Wqkv); l.Y = qkv; l.ldy = QKV;
   l.M = p->B; l.N = QKV; l.K = p->HS; l.norm = 1; l.norm_w = static_cast<const uint16_t*>(p->in_norm_w);
   l.eps = p->eps; l.epi = kEpiStore; l.xn_ws = xn;
-  int rc = launch_linear(l, s);
-  if (rc) return rc;
-
   // q/k RMSNorm + RoPE and the K/V-cache write of the decoded token run in
   // the attention kernel's prologue (attn.hip), reading the bf16 QKV row.
   AttnArgs a{};
@@ -165,7 +162,11 @@ int run_layer(const ezops_qwen3_layer* p, const int32_t* block_table, int64_t nu
   a.cos = static_cast<const uint16_t*>(p->cos);
   a.sin = static_cast<const uint16_t*>(p->sin);
   a.eps = p->eps;
-  rc = launch_attn(a, attn_ws, attn_workspace_size(p->B, p->H, p->Hkv, p->S, p->D), s);
+  // The attention stage's checks before the first launch: a rejected call
+  // leaves nothing queued on the stream.
+  int rc = check_attn(a);
+  if (!rc) rc = launch_linear(l, s);
+  if (!rc) rc = launch_attn(a, attn_ws, attn_workspace_size(p->B, p->H, p->Hkv, p->S, p->D), s);
   if (rc) return rc;
 
   const uint16_t* Wgu = static_cast<const uint16_t*>(p->Wgu);
@@ -229,6 +230,8 @@ extern "C" int ezops_qwen3_decode_step_bf16(const ezops_qwen3_layer* layers, int
                    num_pages <= (int64_t(1) << 31),
                "qwen3_decode_step: page_size must be a power of two >= 32 dividing S");
   }
+  for (int64_t i = 0; i < n_layers; ++i)
+    EZ_REQUIRE(!block_table || layers[i].kv_lens, "qwen3_decode_step: a paged cache requires kv_lens");
   Carve c{static_cast<char*>(ws)};
   uint16_t* hbuf[2] = {c.take<uint16_t>(size_t(l0.B * l0.HS) * 2), c.take<uint16_t>(size_t(l0.B * l0.HS) * 2)};
   void* lws = c.p;
@@ -238,7 +241,6 @@ extern "C" int ezops_qwen3_decode_step_bf16(const ezops_qwen3_layer* layers, int
     ezops_qwen3_layer p = layers[i];
     p.hidden = h;
     if (i + 1 < n_layers) p.out = hbuf[i & 1];
-    EZ_REQUIRE(!block_table || p.kv_lens, "qwen3_decode_step: a paged cache requires kv_lens");
     const int rc = run_layer(&p, block_table, num_pages, page_size, lws, lws_bytes, s);
     if (rc) return rc;
     h = p.out;
@@ -305,10 +307,6 @@ extern "C" int ezops_qwen3_prefill_bf16(const ezops_qwen3_layer* p, int64_t T, c
   const uint16_t* hidden = static_cast<const uint16_t*>(p->hidden);
   auto W = [](const void* q) { return static_cast<const uint16_t*>(q); };
 
-  int rc = ezops_rmsnorm_bf16(hidden, p->in_norm_w, w.xn, T, HS, p->eps, s);
-  if (!rc) rc = gemm_bf16(w.xn, HS, W(p->Wqkv), w.qkv, QKV, nullptr, T, QKV, HS, s);
-  if (rc) return rc;
-
   QkRopeArgs r{};
   r.q = w.qkv; r.q_bs = QKV;
   r.k = w.qkv + QR; r.k_bs = QKV;
@@ -324,8 +322,6 @@ extern "C" int ezops_qwen3_prefill_bf16(const ezops_qwen3_layer* p, int64_t T, c
     r.block_table = block_table; r.bt_stride = p->S / page_size; r.page_size = int(page_size);
     r.num_pages = num_pages;
   }
-  rc = launch_qk_norm_rope(r, s);
-  if (rc) return rc;
 
   PrefillAttnArgs a{};
   a.Q = w.qkv; a.q_rs = QKV;
@@ -336,7 +332,16 @@ extern "C" int ezops_qwen3_prefill_bf16(const ezops_qwen3_layer* p, int64_t T, c
   a.block_table = block_table; a.bt_stride = r.bt_stride; a.page_size = r.page_size; a.num_pages = num_pages;
   a.B = p->B; a.T = T; a.H = p->H; a.Hkv = p->Hkv; a.S = p->S; a.D = p->D; a.max_q = max_q_len;
   a.scale = 0.f;
-  rc = launch_prefill_attn(a, s);
+  // Both stages' checks before the first launch: a rejected call leaves
+  // the cache and the stream untouched.
+  int rc = check_qk_norm_rope(r);
+  if (!rc) rc = check_prefill_attn(a);
+  if (rc) return rc;
+
+  rc = ezops_rmsnorm_bf16(hidden, p->in_norm_w, w.xn, T, HS, p->eps, s);
+  if (!rc) rc = gemm_bf16(w.xn, HS, W(p->Wqkv), w.qkv, QKV, nullptr, T, QKV, HS, s);
+  if (!rc) rc = launch_qk_norm_rope(r, s);
+  if (!rc) rc = launch_prefill_attn(a, s);
   if (!rc) rc = gemm_bf16(w.att, QR, W(p->Wo), w.h, HS, hidden, T, HS, QR, s);
   if (!rc) rc = ezops_rmsnorm_bf16(w.h, p->post_norm_w, w.xn, T, HS, p->eps, s);
   if (!rc) {

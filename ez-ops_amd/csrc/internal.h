@@ -68,6 +68,9 @@ struct QkRopeArgs {
   // Paged cache (block_table != NULL): Kc / Vc are pools [pages, Hkv, page_size, D].
   const int32_t* block_table; int64_t bt_stride; int page_size; int64_t num_pages;
 };
+// check_*: the launcher's argument checks alone (EZ_OK or EZOPS_EINVAL with
+// the error text set), for callers that validate every stage before launching any.
+int check_qk_norm_rope(const QkRopeArgs& a);
 int launch_qk_norm_rope(const QkRopeArgs& a, hipStream_t s);
 
 struct AttnArgs {
@@ -96,6 +99,7 @@ struct AttnArgs {
   float eps;
 };
 size_t attn_workspace_size(int64_t B, int64_t H, int64_t Hkv, int64_t S, int64_t D);
+int check_attn(const AttnArgs& a);
 int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s);
 
 // Prefill attention: new tokens of sequence b are rows cu[b] .. cu[b+1]-1 of
@@ -115,6 +119,7 @@ struct PrefillAttnArgs {
   // rounded to bf16 as the separate QK-norm + RoPE stage rounds it.
   int q_raw; const uint16_t* qw; const uint16_t* qcos; const uint16_t* qsin; float qeps;
 };
+int check_prefill_attn(const PrefillAttnArgs& a);
 int launch_prefill_attn(const PrefillAttnArgs& a, hipStream_t s);
 int launch_silu_mul(const uint16_t* gu, uint16_t* out, int64_t T, int64_t IS, hipStream_t s);
 

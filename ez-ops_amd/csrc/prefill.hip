@@ -465,7 +465,23 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* gu, uint1
 
 }  // namespace
 
-int launch_prefill_attn(const PrefillAttnArgs& a, hipStream_t s) {
+namespace {
+// Grid of the prefill attention: query tiles of bq = 32 kPW / hpb rows
+// (hpb = heads per block) per (sequence, kv head, head group).
+int prefill_qtiles(const PrefillAttnArgs& a) {
+  const int64_t G = a.H / a.Hkv;
+  const int hpb = G < 4 ? int(G) : 4;
+  const int bq = 32 * kPW / hpb;
+  return int((a.max_q + bq - 1) / bq);
+}
+int64_t prefill_blocks(const PrefillAttnArgs& a) {
+  const int64_t G = a.H / a.Hkv;
+  const int hpb = G < 4 ? int(G) : 4;
+  return int64_t(prefill_qtiles(a)) * a.B * a.Hkv * (G / hpb);
+}
+}  // namespace
+
+int check_prefill_attn(const PrefillAttnArgs& a) {
   EZ_REQUIRE(a.Q && a.K && a.V && a.Out && a.cu, "prefill_attn: null pointer");
   EZ_REQUIRE(a.B >= 1 && a.T >= 0 && a.H >= 1 && a.Hkv >= 1 && a.S >= 1 && a.max_q >= 0, "prefill_attn: bad shape");
   EZ_REQUIRE(a.D == kPD, "prefill_attn: head_dim must be %d", kPD);
@@ -481,14 +497,19 @@ int launch_prefill_attn(const PrefillAttnArgs& a, hipStream_t s) {
   EZ_REQUIRE(!a.q_raw || ((a.qcos == nullptr) == (a.qsin == nullptr) && (!a.qw || aligned16(a.qw)) &&
                           (!a.qcos || (aligned16(a.qcos) && aligned16(a.qsin)))),
              "prefill_attn: q norm weight and cos / sin tables must be 16-byte aligned, cos and sin together");
+  EZ_REQUIRE(prefill_blocks(a) < (int64_t(1) << 31), "prefill_attn: grid too large");
+  return EZ_OK;
+}
+
+int launch_prefill_attn(const PrefillAttnArgs& a, hipStream_t s) {
+  const int rc = check_prefill_attn(a);
+  if (rc != EZ_OK) return rc;
   if (a.max_q == 0) return 0;
   PrefillAttnArgs aa = a;
   if (aa.scale <= 0.f) aa.scale = 1.f / sqrtf(float(kPD));
-  const int hpb = G < 4 ? int(G) : 4;
-  const int bq = 32 * kPW / hpb;
-  const int ntq = int((a.max_q + bq - 1) / bq);
-  const int64_t blocks = int64_t(ntq) * a.B * a.Hkv * (G / hpb);
-  EZ_REQUIRE(blocks < (int64_t(1) << 31), "prefill_attn: grid too large");
+  const int64_t G = a.H / a.Hkv;
+  const int ntq = prefill_qtiles(a);
+  const int64_t blocks = prefill_blocks(a);
   const dim3 grid{unsigned(blocks)}, block{unsigned(kPW * kWave)};
 #define EZ_PF(GG)                                                                                    \
   if (a.block_table) hipLaunchKernelGGL((prefill_attn_kernel<GG, true>), grid, block, 0, s, aa, ntq); \

@@ -183,7 +183,16 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 }  // namespace
 
-int launch_qk_norm_rope(const QkRopeArgs& a, hipStream_t s) {
+namespace {
+bool vec_form(const QkRopeArgs& a) {
+  return (a.D == 64 || a.D == 128 || a.D == 256) && a.q_bs % 8 == 0 && a.k_bs % 8 == 0 && a.v_bs % 8 == 0 &&
+         aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.Kc) && aligned16(a.Vc) &&
+         (!a.q_out || aligned16(a.q_out)) && (!a.k_out || aligned16(a.k_out)) && (!a.qw || aligned16(a.qw)) &&
+         (!a.kw || aligned16(a.kw)) && (!a.cos || aligned16(a.cos)) && (!a.sin || aligned16(a.sin));
+}
+}  // namespace
+
+int check_qk_norm_rope(const QkRopeArgs& a) {
   EZ_REQUIRE(a.q && a.k && a.v && a.Kc && a.Vc, "qk_norm_rope: null pointer");
   EZ_REQUIRE(a.B >= 1 && a.H >= 1 && a.Hkv >= 1 && a.S >= 1, "qk_norm_rope: bad shape");
   EZ_REQUIRE(a.D >= 2 && a.D <= 2 * kMaxPairsPerLane * kWave && a.D % 2 == 0,
@@ -193,12 +202,15 @@ int launch_qk_norm_rope(const QkRopeArgs& a, hipStream_t s) {
   EZ_REQUIRE(!a.block_table || (a.page_size >= 1 && (a.page_size & (a.page_size - 1)) == 0 && a.num_pages >= 1 &&
                                 a.S == a.bt_stride * a.page_size),
              "qk_norm_rope: paged cache needs a power-of-two page_size and S = max_pages * page_size");
+  EZ_REQUIRE(a.q_out || vec_form(a), "qk_norm_rope: the k / v-only form needs head_dim 64, 128 or 256 and 16-byte rows");
+  return EZ_OK;
+}
+
+int launch_qk_norm_rope(const QkRopeArgs& a, hipStream_t s) {
+  const int rc = check_qk_norm_rope(a);
+  if (rc != EZ_OK) return rc;
   const int64_t heads = a.B * (a.q_out ? a.H + a.Hkv : a.Hkv);
-  const bool vec = (a.D == 64 || a.D == 128 || a.D == 256) && a.q_bs % 8 == 0 && a.k_bs % 8 == 0 &&
-                   a.v_bs % 8 == 0 && aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.Kc) &&
-                   aligned16(a.Vc) && (!a.q_out || aligned16(a.q_out)) && (!a.k_out || aligned16(a.k_out)) &&
-                   (!a.qw || aligned16(a.qw)) && (!a.kw || aligned16(a.kw)) && (!a.cos || aligned16(a.cos)) &&
-                   (!a.sin || aligned16(a.sin));
+  const bool vec = vec_form(a);
   if (vec) {
     const int64_t hpw = kWave / (a.D / 8);
     const unsigned blocks = unsigned((heads + 4 * hpw - 1) / (4 * hpw));
@@ -206,7 +218,6 @@ int launch_qk_norm_rope(const QkRopeArgs& a, hipStream_t s) {
     else if (a.D == 128) hipLaunchKernelGGL(qk_norm_rope_vec_kernel<128>, dim3(blocks), dim3(256), 0, s, a);
     else hipLaunchKernelGGL(qk_norm_rope_vec_kernel<256>, dim3(blocks), dim3(256), 0, s, a);
   } else {
-    EZ_REQUIRE(a.q_out, "qk_norm_rope: the k / v-only form needs head_dim 64, 128 or 256 and 16-byte rows");
     hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(unsigned((heads + 3) / 4)), dim3(256), 0, s, a);
   }
   return launch_status("qk_norm_rope");

@@ -99,3 +99,37 @@ def test_new_entry_points_reject_bad_arguments():
     same = (_hip.Qwen3LayerParams * 1)()
     same[0] = _hip.Qwen3LayerParams(B=1, S=128, HS=256, IS=512, H=4, Hkv=2, D=128, hidden=d, out=d)
     assert lib.ezops_qwen3_decode_step_bf16(same, 1, d, 4, 48, None, None, 0, None, d, 1 << 30, None) == _hip.EINVAL
+
+
+def test_layer_entries_reject_before_any_launch():
+    """Every stage's limits are checked before the first launch, so these
+    return EINVAL on a machine without a GPU (a launch would fail with a
+    device error instead) and, on a GPU, leave the cache and stream untouched."""
+    lib = _hip.lib()
+    d = 4096  # a 16-byte aligned non-null address that is never touched
+    ptrs = dict(hidden=d, K_cache=d, V_cache=d, Wqkv=d, Wo=d, Wgu=d, Wd=d, out=d)
+
+    def layer(**kw):
+        shape = dict(B=1, S=128, HS=256, IS=512, H=4, Hkv=2, D=128)
+        shape.update(kw)
+        return _hip.Qwen3LayerParams(**shape, **ptrs)
+
+    # decode layer: the attention stage's head_dim, group size and length bound
+    for kw, text in [(dict(D=96), b"head_dim"), (dict(H=64, Hkv=2), b"group size"),
+                     (dict(max_kv_len=-1), b"max_kv_len")]:
+        rc = lib.ezops_qwen3_dense_decode_bf16(ctypes.byref(layer(**kw)), d, 1 << 30, None)
+        assert rc == _hip.EINVAL and text in lib.ezops_hip_last_error(), (kw, lib.ezops_hip_last_error())
+    # decode step over a paged cache: a later layer without kv_lens
+    layers = (_hip.Qwen3LayerParams * 2)(layer(kv_lens=d), layer())
+    rc = lib.ezops_qwen3_decode_step_bf16(layers, 2, d, 8, 64, None, None, 0, None, d, 1 << 30, None)
+    assert rc == _hip.EINVAL and b"kv_lens" in lib.ezops_hip_last_error()
+    # prefill: the attention stage's head_dim, group size, cache bound and alignment
+    cu = d
+    for kw, text in [(dict(D=64), b"head_dim"), (dict(H=32, Hkv=2), b"group size"),
+                     (dict(S=1 << 23), b"2^23")]:
+        rc = lib.ezops_qwen3_prefill_bf16(ctypes.byref(layer(**kw)), 16, cu, 16, None, 0, 0, d, 1 << 40, None)
+        assert rc == _hip.EINVAL and text in lib.ezops_hip_last_error(), (kw, lib.ezops_hip_last_error())
+    p = layer()
+    p.K_cache = d + 2
+    rc = lib.ezops_qwen3_prefill_bf16(ctypes.byref(p), 16, cu, 16, None, 0, 0, d, 1 << 40, None)
+    assert rc == _hip.EINVAL and b"16-byte" in lib.ezops_hip_last_error()
