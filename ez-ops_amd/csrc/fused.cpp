@@ -34,7 +34,11 @@ struct Carve {
 };
 
 // Batched (B > 4) stages hand activations to the next MFMA GEMM in its
-// packed operand layout when the width allows it.
+// packed operand layout when the width allows it and the stages on both
+// sides take their vector path (16-byte aligned weights, rows of whole
+// 16-byte chunks); otherwise row-major, so no stage can reject the layout
+// after earlier stages have run.
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 bool packable(int64_t B, int64_t K) { return B > 4 && K % 32 == 0; }
 
 size_t ffn_ws(int64_t B, int64_t HS, int64_t IS) {
@@ -50,7 +54,7 @@ int run_ffn(const uint16_t* attn, bool attn_packed, const uint16_t* residual, co
   uint16_t* x2 = c.take<uint16_t>(size_t(B * HS) * 2);
   uint16_t* h = c.take<uint16_t>(size_t(packed_rows(B) * IS) * 2);
   uint16_t* xn = c.take<uint16_t>(size_t(packed_rows(B) * HS) * 2);  // staged RMSNorm input (batch > 4)
-  const bool hp = packable(B, IS);
+  const bool hp = packable(B, IS) && HS % 8 == 0 && al16(Wg) && al16(Wu) && al16(Wd) && (!post_w || al16(post_w));
 
   LinearArgs o{};
   o.X = attn; o.ldx = QR; o.x_packed = attn_packed; o.W = Wo; o.Y = x2; o.ldy = HS;
@@ -129,7 +133,7 @@ int run_layer(const ezops_qwen3_layer* p, const int32_t* block_table, int64_t nu
   uint16_t* xn = c.take<uint16_t>(size_t(packed_rows(p->B) * p->HS) * 2);
   uint16_t* qkv = c.take<uint16_t>(size_t(p->B * QKV) * 2);
   uint16_t* att = c.take<uint16_t>(size_t(packed_rows(p->B) * QR) * 2);
-  const bool att_packed = packable(p->B, QR);
+  const bool att_packed = packable(p->B, QR) && al16(p->Wo);
   char* attn_ws = c.take<char>(attn_workspace_size(p->B, p->H, p->Hkv, p->S, p->D));
   char* ffn = c.p;
 

@@ -91,10 +91,21 @@ def test_fused_o_proj_ffn(batch, shape):
     np.testing.assert_allclose(n(out), n(ref), **BF_TOL)
 
 
-def _layer(batch, seq_len, kwargs, **mode):
+def _misaligned(t):
+    """The same values at an address 2 bytes past a 16-byte boundary."""
+    buf = torch.empty(t.numel() + 8, dtype=t.dtype, device=t.device)
+    v = buf[1:1 + t.numel()].view(t.shape)
+    v.copy_(t)
+    assert v.data_ptr() % 16 != 0
+    return v
+
+
+def _layer(batch, seq_len, kwargs, misalign=(), **mode):
     torch.manual_seed(42)
     op = Qwen3DenseDecodeOp(batch, seq_len, backend="hip", **kwargs, **mode)
-    data = op.gen_data()
+    data = list(op.gen_data())
+    for i in misalign:
+        data[i] = _misaligned(data[i])
     K0, V0 = data[1].clone(), data[2].clone()
     out = op(*data)
     npy = [n(x) for x in data]
@@ -129,6 +140,28 @@ def test_qwen3_8b_layer_qwen3_mode(batch, seq_len):
     rng = np.random.default_rng(4)
     lens = rng.integers(min(1024, seq_len), seq_len + 1, size=batch).tolist()
     _layer(batch, seq_len, {**QWEN3_8B, "num_kv_heads": 8}, kv_lens=lens, norm_weights=True, rope_theta=1e6)
+
+
+@pytest.mark.parametrize("misalign", [(4,), (5,), (6,), (4, 5, 6)])  # Wo, Wgu, Wd
+def test_batched_layer_unaligned_weights(misalign):
+    """At batch > 4 the stages pass activations on in the MFMA-packed layout
+    only when the stages on both sides read it with 16-byte loads; an
+    unaligned weight selects the row-major hand-off (the layer used to return
+    EINVAL from a middle stage after the cache write)."""
+    _layer(8, 512, {**QWEN3_0_6B, "num_kv_heads": 8}, misalign=misalign, kv_lens=[500, 17, 300, 512, 1, 64, 255, 400],
+           norm_weights=True, rope_theta=1e6)
+
+
+@pytest.mark.parametrize("misalign", [(2,), (4, 5), (6,)])  # Wo, Wg / Wu, Wd
+def test_batched_o_proj_ffn_unaligned_weights(misalign):
+    torch.manual_seed(42)
+    op = FusedOProjFfnOp(16, backend="hip", **QWEN3_0_6B)
+    data = list(op.gen_data())
+    for i in misalign:
+        data[i] = _misaligned(data[i])
+    out = op(*data)
+    ref = oracle.o_proj_ffn(*[n(x) for x in data])
+    np.testing.assert_allclose(n(out), ref, **BF_TOL)
 
 
 def test_qwen3_layer_repeated_calls():
