@@ -773,6 +773,7 @@ int launch_attn(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
   if (pl.nsplit > 1) {
     const size_t need = attn_workspace_size(a.B, a.H, a.Hkv, a.S, a.D);
     EZ_REQUIRE(ws && ws_bytes >= need, "attn_decode: workspace too small (%zu < %zu)", ws_bytes, need);
+    EZ_REQUIRE((reinterpret_cast<uintptr_t>(ws) & 15) == 0, "attn_decode: workspace must be 16-byte aligned");
     opart = static_cast<float*>(ws);
     ml = reinterpret_cast<float*>(static_cast<char*>(ws) + align256(size_t(a.B * a.H * pl.nsplit * a.D) * 4));
   }

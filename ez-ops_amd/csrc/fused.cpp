@@ -91,7 +91,7 @@ extern "C" int ezops_o_proj_ffn_bf16(const void* attn, const void* residual, con
                                      int64_t QR, float eps, void* ws, size_t ws_bytes, hipStream_t s) {
   EZ_REQUIRE(attn && residual && Wo && Wg && Wu && Wd && out && ws, "o_proj_ffn: null pointer");
   EZ_REQUIRE(B >= 1 && HS >= 1 && IS >= 1 && QR >= 1, "o_proj_ffn: bad shape");
-  EZ_REQUIRE(ws_bytes >= ffn_ws(B, HS, IS), "o_proj_ffn: workspace too small");
+  EZ_REQUIRE(ws_bytes >= ffn_ws(B, HS, IS) && al16(ws), "o_proj_ffn: workspace too small or not 16-byte aligned");
   return run_ffn(static_cast<const uint16_t*>(attn), false, static_cast<const uint16_t*>(residual),
                  static_cast<const uint16_t*>(Wo), static_cast<const uint16_t*>(post_norm_w),
                  static_cast<const uint16_t*>(Wg), static_cast<const uint16_t*>(Wu),
@@ -127,7 +127,8 @@ int run_layer(const ezops_qwen3_layer* p, const int32_t* block_table, int64_t nu
              "qwen3_dense_decode: bad shape");
   EZ_REQUIRE(p->H % p->Hkv == 0, "qwen3_dense_decode: num_heads must be divisible by num_kv_heads");
   EZ_REQUIRE((p->cos == nullptr) == (p->sin == nullptr), "qwen3_dense_decode: cos and sin go together");
-  EZ_REQUIRE(ws_bytes >= ezops_qwen3_layer_workspace_size(p), "qwen3_dense_decode: workspace too small");
+  EZ_REQUIRE(ws_bytes >= ezops_qwen3_layer_workspace_size(p) && al16(ws),
+             "qwen3_dense_decode: workspace too small or not 16-byte aligned");
   const int64_t QR = p->H * p->D, KVR = p->Hkv * p->D, QKV = QR + 2 * KVR;
   Carve c{static_cast<char*>(ws)};
   uint16_t* xn = c.take<uint16_t>(size_t(packed_rows(p->B) * p->HS) * 2);
@@ -227,8 +228,8 @@ extern "C" int ezops_qwen3_decode_step_bf16(const ezops_qwen3_layer* layers, int
   EZ_REQUIRE(vocab >= 0 && (vocab == 0 || (lm_head && logits)), "qwen3_decode_step: lm_head and logits go with vocab > 0");
   for (int64_t i = 1; i < n_layers; ++i)
     EZ_REQUIRE(same_shape(l0, layers[i]), "qwen3_decode_step: layer %lld shape differs from layer 0", (long long)i);
-  EZ_REQUIRE(ws_bytes >= ezops_qwen3_decode_step_workspace_size(layers, n_layers, vocab),
-             "qwen3_decode_step: workspace too small");
+  EZ_REQUIRE(ws_bytes >= ezops_qwen3_decode_step_workspace_size(layers, n_layers, vocab) && al16(ws),
+             "qwen3_decode_step: workspace too small or not 16-byte aligned");
   if (block_table) {
     EZ_REQUIRE(page_size >= 32 && (page_size & (page_size - 1)) == 0 && l0.S % page_size == 0 && num_pages >= 1 &&
                    num_pages <= (int64_t(1) << 31),
@@ -301,7 +302,8 @@ extern "C" int ezops_qwen3_prefill_bf16(const ezops_qwen3_layer* p, int64_t T, c
                  p->Hkv >= 1 && p->H % p->Hkv == 0 && max_q_len >= 1,
              "qwen3_prefill: bad shape");
   EZ_REQUIRE((p->cos == nullptr) == (p->sin == nullptr), "qwen3_prefill: cos and sin go together");
-  EZ_REQUIRE(ws_bytes >= ezops_qwen3_prefill_workspace_size(p, T), "qwen3_prefill: workspace too small");
+  EZ_REQUIRE(ws_bytes >= ezops_qwen3_prefill_workspace_size(p, T) && al16(ws),
+             "qwen3_prefill: workspace too small or not 16-byte aligned");
   if (block_table)
     EZ_REQUIRE(page_size >= 32 && (page_size & (page_size - 1)) == 0 && p->S % page_size == 0 && num_pages >= 1,
                "qwen3_prefill: page_size must be a power of two >= 32 dividing S");

@@ -1126,10 +1126,11 @@ int launch_linear(const LinearArgs& a, hipStream_t s) {
     // the per-tile kernel repeats the work in every block of 16 weight rows:
     // measured slower than staging).
     LinearArgs b = a;
+    EZ_REQUIRE(!a.norm || (a.xn_ws && aligned16(a.xn_ws)),
+               "linear: RMSNorm prologue with M > 4 needs a 16-byte aligned workspace (ezops_linear_stage_workspace_size)");
+    EZ_REQUIRE(!a.norm || (!a.x_packed && a.ldx == a.K), "linear: RMSNorm prologue with M > 4 needs contiguous X rows");
     if (a.norm && launch_xs_norm(a, s)) return launch_status("linear");
     if (a.norm) {
-      EZ_REQUIRE(a.xn_ws, "linear: RMSNorm prologue with M > 4 needs a workspace (ezops_linear_stage_workspace_size)");
-      EZ_REQUIRE(!a.x_packed && a.ldx == a.K, "linear: RMSNorm prologue with M > 4 needs contiguous X rows");
       int rc;
       if (a.K % 32 == 0) {  // staged straight into the MFMA-packed layout
         rc = launch_rmsnorm_bf16_packed(a.X, a.norm_w, a.xn_ws, a.M, a.K, a.eps, s);

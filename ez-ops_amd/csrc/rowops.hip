@@ -436,6 +436,7 @@ extern "C" int ezops_reduce_sum_f32(const float* A, float* Out, int64_t n, void*
   EZ_REQUIRE(A && Out && ws, "reduce_sum_f32: null pointer");
   EZ_REQUIRE(n >= 1, "reduce_sum_f32: n must be >= 1");
   EZ_REQUIRE(ws_bytes >= ezops_reduce_sum_workspace_size(n), "reduce_sum_f32: workspace too small");
+  EZ_REQUIRE(aligned16(ws), "reduce_sum_f32: workspace must be 16-byte aligned");
   const int64_t G = sum_blocks(n);
   int* counter = static_cast<int*>(ws);
   float* partial = reinterpret_cast<float*>(static_cast<char*>(ws) + 256);

@@ -9,7 +9,8 @@
  *   - Work is enqueued on `stream`; nothing synchronises, allocates or reads
  *     device memory back, so every call can be captured into a HIP graph.
  *   - Scratch memory is caller-owned: `*_workspace_size` gives the byte count
- *     and the caller passes a zero-filled buffer of at least that size once;
+ *     and the caller passes a zero-filled, 16-byte aligned buffer of at least
+ *     that size once;
  *     the kernels leave their counters at zero again after every call, so
  *     the same workspace serves later calls on the same stream.  Calls that
  *     overlap in time must not share a workspace.
@@ -61,7 +62,8 @@ int ezops_linear_bf16(const void* X, int64_t ldx, const void* W, void* Y, int64_
  * (norm_w NULL = unit).  epilogue 0: Y = bf16(acc); 1: Y = bf16(res + bf16(acc));
  * 2: SwiGLU, W2 holds the up rows: Y = bf16(bf16(silu(bf16(g))) * bf16(u));
  * 3: Y = acc as fp32.  With norm and M > 4 the normalised input is staged in
- * the workspace (ezops_linear_stage_workspace_size bytes; X rows contiguous).
+ * the workspace (ezops_linear_stage_workspace_size bytes, 16-byte aligned;
+ * X rows contiguous).
  * Replaces: the per-stage kernels of the reference's multi-launch fused
  * variants (ezops/kernels/fused_o_proj_ffn/fused_o_proj_ffn_tl.py:49-250,
  * ezops/kernels/qwen3_dense_decode/qwen3_dense_decode_multilaunch_tl.py:68-588). */

@@ -133,3 +133,32 @@ def test_layer_entries_reject_before_any_launch():
     p.K_cache = d + 2
     rc = lib.ezops_qwen3_prefill_bf16(ctypes.byref(p), 16, cu, 16, None, 0, 0, d, 1 << 40, None)
     assert rc == _hip.EINVAL and b"16-byte" in lib.ezops_hip_last_error()
+
+
+def test_linear_stage_rejects_unaligned_staging_workspace():
+    lib = _hip.lib()
+    d = 4096
+    need = lib.ezops_linear_stage_workspace_size(8, 256, 1)
+    rc = lib.ezops_linear_stage_bf16(d, 256, d, None, d, 64, None, 0, None, 1, 1e-6, 0, 8, 64, 256, d + 2, need, None)
+    assert rc == _hip.EINVAL and b"16-byte aligned workspace" in lib.ezops_hip_last_error()
+
+
+def test_workspaces_must_be_16_byte_aligned():
+    lib = _hip.lib()
+    d, odd = 4096, 4096 + 4
+    assert lib.ezops_reduce_sum_f32(d, d, 1 << 20, odd, 1 << 30, None) == _hip.EINVAL
+    assert b"aligned" in lib.ezops_hip_last_error()
+    assert lib.ezops_attn_decode_bf16(d, d, d, d, 8, 32, 8, 8192, 128, None, 0, 0.0, odd, 1 << 30, None) == _hip.EINVAL
+    assert b"aligned" in lib.ezops_hip_last_error()
+    assert lib.ezops_o_proj_ffn_bf16(d, d, d, None, d, d, d, d, 1, 4096, 12288, 4096, 1e-6, odd, 1 << 30,
+                                     None) == _hip.EINVAL
+    assert b"aligned" in lib.ezops_hip_last_error()
+    p = _hip.Qwen3LayerParams(B=1, S=128, HS=256, IS=512, H=4, Hkv=2, D=128, hidden=d, K_cache=d, V_cache=d,
+                              Wqkv=d, Wo=d, Wgu=d, Wd=d, out=d)
+    assert lib.ezops_qwen3_dense_decode_bf16(ctypes.byref(p), odd, 1 << 30, None) == _hip.EINVAL
+    assert b"aligned" in lib.ezops_hip_last_error()
+    assert lib.ezops_qwen3_decode_step_bf16((_hip.Qwen3LayerParams * 1)(p), 1, None, 0, 0, None, None, 0, None,
+                                            odd, 1 << 30, None) == _hip.EINVAL
+    assert b"aligned" in lib.ezops_hip_last_error()
+    assert lib.ezops_qwen3_prefill_bf16(ctypes.byref(p), 16, d, 16, None, 0, 0, odd, 1 << 30, None) == _hip.EINVAL
+    assert b"aligned" in lib.ezops_hip_last_error()
