@@ -1100,6 +1100,9 @@ int launch_linear(const LinearArgs& a, hipStream_t s) {
   EZ_REQUIRE(a.epi != kEpiSilu || a.W2, "linear: SwiGLU epilogue needs the up-projection weights");
   EZ_REQUIRE(a.epi != kEpiResid || a.res, "linear: residual epilogue needs the residual");
   EZ_REQUIRE(a.N < (int64_t(1) << 31) / 16 && a.M < 65536 * 16, "linear: sizes too large");
+  // The batched kernels address a 16-row weight tile through a buffer
+  // resource with 32-bit extents (16 K bf16 < 2^31 bytes).
+  EZ_REQUIRE(a.M <= 4 || a.K < (int64_t(1) << 26), "linear: K must be below 2^26 for batch > 4");
   EZ_REQUIRE(!(a.x_packed || a.y_packed) || a.M > 4, "linear: the packed layouts are for M > 4");
   EZ_REQUIRE(!a.x_packed || a.K % 32 == 0, "linear: packed X needs K %% 32 == 0");
   EZ_REQUIRE(!a.y_packed || (a.N % 32 == 0 && a.ldy == a.N && a.epi != kEpiStoreF32),

@@ -162,3 +162,10 @@ def test_workspaces_must_be_16_byte_aligned():
     assert b"aligned" in lib.ezops_hip_last_error()
     assert lib.ezops_qwen3_prefill_bf16(ctypes.byref(p), 16, d, 16, None, 0, 0, odd, 1 << 30, None) == _hip.EINVAL
     assert b"aligned" in lib.ezops_hip_last_error()
+
+
+def test_batched_linear_rejects_huge_k():
+    lib = _hip.lib()
+    d, K = 4096, 1 << 26
+    rc = lib.ezops_linear_bf16(d, K, d, d, 16, 8, 16, K, None)
+    assert rc == _hip.EINVAL and b"2^26" in lib.ezops_hip_last_error()
