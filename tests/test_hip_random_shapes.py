@@ -7,7 +7,12 @@ GEMV, X-stationary and DMA-ring MFMA kernels), widths with and without a
 masked last chunk, every epilogue, RMSNorm on and off, padded X rows.
 GEMM: M, N up to ~2K, K % 8 == 0 (the MFMA kernel, masked last K-step) and
 K % 8 != 0 (the linear-layer kernels), padded rows, residual on and off.
-Bar: bf16 allclose(atol 2e-2, rtol 1e-2) against the fp32-accumulated oracle.
+Decode attention: batch, group size, head_dim, capacity, ragged lengths and
+length bounds.  The whole decode layer: batch 1-20, group sizes 1-16,
+head_dim 64 / 128, widths, contiguous or paged caches.  Prefill attention:
+chunk lengths (empty ones included), cached prefixes, groups, paging.
+Bar: bf16 allclose(atol 2e-2, rtol 1e-2) against the fp32-accumulated
+oracle (the layer: that bar with the oracle's own accumulation-order slack).
 """
 
 import numpy as np
@@ -115,3 +120,88 @@ def test_attn_decode_random(seed):
               tl.data_ptr(), hint, 0.0, ws.data_ptr(), ws.numel(), _hip.stream())
     ref = oracle.attn_decode(n(Q), n(K), n(V), kv_lens=lens)
     np.testing.assert_allclose(n(out), ref, **BF_TOL, err_msg=f"B={B} H={H} Hkv={Hkv} S={S} D={D} hint={hint}")
+
+
+# ---- whole decode layer and prefill attention
+from ezops import PrefillAttnOp, Qwen3DenseDecodeOp  # noqa: E402
+
+
+def _layer_bar(out, ref, msg):
+    """The layer's bar: the elementwise bf16 bar on all but at most
+    max(2, 1e-4 n) elements and every element within twice it (fp32
+    accumulation orders of the oracle itself differ past the bar on single
+    elements of a layer; tests/test_oracle.py::test_layer_bar_order_sensitivity)."""
+    d = np.abs(out - ref)
+    bar = BF_TOL["atol"] + BF_TOL["rtol"] * np.abs(ref)
+    assert (d <= 2 * bar).all(), (msg, float((d - 2 * bar).max()))
+    assert int((d > bar).sum()) <= max(2, int(1e-4 * d.size)), (msg, int((d > bar).sum()))
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_qwen3_layer_random(seed):
+    """The decode layer over random batch (1-20: row-block GEMV, MFMA and
+    X-stationary stages), group size, head_dim, widths, capacity and ragged
+    lengths, contiguous or paged, with weighted norms and RoPE, against the
+    oracle layer; the decoded token's k / v land in their cache rows."""
+    rng = np.random.default_rng(5000 + seed)
+    B = int(rng.integers(1, 21))
+    G = int(rng.choice([1, 2, 4, 8, 16]))
+    Hkv = int(rng.choice([1, 2, 4])) if G < 16 else int(rng.choice([1, 2]))
+    H, D = G * Hkv, int(rng.choice([64, 128]))
+    HS = int(rng.choice([256, 512, 1024, 2048]))
+    IS = int(rng.choice([512, 1024, 1536, 3072]))
+    paged = bool(rng.integers(0, 2))
+    ps = int(rng.choice([32, 64])) if paged else None
+    S = int(rng.integers(2, 33)) * (ps or 64)
+    lens = rng.integers(1, S + 1, size=B).tolist()
+    msg = f"B={B} H={H} Hkv={Hkv} D={D} HS={HS} IS={IS} S={S} page={ps}"
+    torch.manual_seed(seed)
+    kw = dict(page_size=ps, num_pages=B * (S // ps) + 3) if paged else {}
+    op = Qwen3DenseDecodeOp(B, S, HS, IS, H, D, backend="hip", num_kv_heads=Hkv, kv_lens=lens, norm_weights=True,
+                            rope_theta=1e6, **kw)
+    data = list(op.gen_data(DEV))
+    K0, V0 = n(data[1]), n(data[2])
+    out = op(*data)
+    npy = [n(x) for x in data[:13]]
+    if paged:
+        bt = data[13].cpu().numpy()
+        K0, V0 = oracle.paged_to_contiguous(K0, bt, ps), oracle.paged_to_contiguous(V0, bt, ps)
+        Kw = oracle.paged_to_contiguous(n(data[1]), bt, ps)
+    else:
+        Kw = n(data[1])
+    ref, rK, _ = oracle.qwen3_layer(npy[0], K0, V0, *npy[3:7], H, Hkv, D, kv_lens=lens, in_norm_w=npy[7],
+                                    q_norm_w=npy[8], k_norm_w=npy[9], post_norm_w=npy[10], cos=npy[11], sin=npy[12])
+    _layer_bar(n(out), ref, msg)
+    for b, L in enumerate(lens):
+        np.testing.assert_allclose(Kw[b, :, L - 1], rK[b, :, L - 1], **BF_TOL, err_msg=msg)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_prefill_attn_random(seed):
+    """Prefill attention over random sequence counts, chunk lengths (empty
+    chunks included), cached prefixes, group sizes and capacities, contiguous
+    or paged, against the oracle."""
+    rng = np.random.default_rng(6000 + seed)
+    B = int(rng.integers(1, 5))
+    G = int(rng.choice([1, 2, 4, 8]))
+    Hkv = int(rng.choice([1, 2, 4]))
+    paged = bool(rng.integers(0, 2))
+    ps = int(rng.choice([32, 64, 128])) if paged else None
+    S = int(rng.integers(2, 25)) * (ps or 64)
+    q_lens = [int(rng.integers(0, min(S, 300) + 1)) for _ in range(B)]
+    past = [int(rng.integers(0, S - q + 1)) for q in q_lens]
+    if sum(q_lens) == 0:
+        q_lens[0] = 1
+        past[0] = min(past[0], S - 1)
+    msg = f"B={B} G={G} Hkv={Hkv} S={S} q={q_lens} past={past} page={ps}"
+    torch.manual_seed(seed)
+    kw = dict(page_size=ps, num_pages=B * (S // ps) + 2) if paged else {}
+    op = PrefillAttnOp(B, G * Hkv, Hkv, 128, S, q_lens, past, backend="hip", **kw)
+    data = list(op.gen_data(DEV))
+    out = op(*data)
+    K, V = n(data[1]), n(data[2])
+    if paged:
+        bt = data[3].cpu().numpy()
+        K, V = oracle.paged_to_contiguous(K, bt, ps), oracle.paged_to_contiguous(V, bt, ps)
+    ref = oracle.prefill_attn(n(data[0]), K, V, q_lens, past)
+    np.testing.assert_allclose(n(out), ref, **BF_TOL, err_msg=msg)
