@@ -10,7 +10,8 @@ K % 8 != 0 (the linear-layer kernels), padded rows, residual on and off.
 Decode attention: batch, group size, head_dim, capacity, ragged lengths and
 length bounds.  The whole decode layer: batch 1-20, group sizes 1-16,
 head_dim 64 / 128, widths, contiguous or paged caches.  Prefill attention:
-chunk lengths (empty ones included), cached prefixes, groups, paging.
+chunk lengths (empty ones included), cached prefixes, groups, paging; the
+prefill layer likewise, with widths that take the separate SwiGLU pass.
 Bar: bf16 allclose(atol 2e-2, rtol 1e-2) against the fp32-accumulated
 oracle (the layer: that bar with the oracle's own accumulation-order slack).
 """
@@ -205,3 +206,47 @@ def test_prefill_attn_random(seed):
         K, V = oracle.paged_to_contiguous(K, bt, ps), oracle.paged_to_contiguous(V, bt, ps)
     ref = oracle.prefill_attn(n(data[0]), K, V, q_lens, past)
     np.testing.assert_allclose(n(out), ref, **BF_TOL, err_msg=msg)
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_qwen3_prefill_random(seed):
+    """The prefill layer over random sequence counts, chunk lengths (empty
+    chunks included), cached prefixes, group sizes, widths (IS % 128 != 0:
+    the separate SwiGLU pass) and paging, against the oracle: the output and
+    every cache row the chunk writes."""
+    from ezops import Qwen3PrefillOp
+
+    rng = np.random.default_rng(7000 + seed)
+    B = int(rng.integers(1, 4))
+    G = int(rng.choice([1, 2, 4, 8]))
+    Hkv = int(rng.choice([1, 2, 4]))
+    HS = int(rng.choice([256, 512, 1024]))
+    IS = int(rng.choice([512, 768, 1000, 1536]))
+    paged = bool(rng.integers(0, 2))
+    ps = int(rng.choice([32, 64])) if paged else None
+    S = int(rng.integers(4, 17)) * (ps or 64)
+    q_lens = [int(rng.integers(0, min(S, 200) + 1)) for _ in range(B)]
+    if sum(q_lens) == 0:
+        q_lens[0] = 1
+    past = [int(rng.integers(0, S - q + 1)) for q in q_lens]
+    msg = f"B={B} G={G} Hkv={Hkv} HS={HS} IS={IS} S={S} q={q_lens} past={past} page={ps}"
+    torch.manual_seed(seed)
+    kw = dict(page_size=ps, num_pages=B * (S // ps) + 2) if paged else {}
+    op = Qwen3PrefillOp(B, S, HS, IS, G * Hkv, 128, q_lens, past, backend="hip", num_kv_heads=Hkv, norm_weights=True,
+                        rope_theta=1e6, **kw)
+    data = list(op.gen_data(DEV))
+    K0, V0 = n(data[1]), n(data[2])
+    out = op(*data)
+    Kw, Vw = n(data[1]), n(data[2])
+    if paged:
+        bt = data[13].cpu().numpy()
+        K0, V0 = oracle.paged_to_contiguous(K0, bt, ps), oracle.paged_to_contiguous(V0, bt, ps)
+        Kw, Vw = oracle.paged_to_contiguous(Kw, bt, ps), oracle.paged_to_contiguous(Vw, bt, ps)
+    npy = [n(x) for x in data[:13]]
+    ref, rK, rV = oracle.qwen3_prefill(npy[0], K0, V0, *npy[3:7], G * Hkv, Hkv, 128, q_lens, past, in_norm_w=npy[7],
+                                       q_norm_w=npy[8], k_norm_w=npy[9], post_norm_w=npy[10], cos=npy[11],
+                                       sin=npy[12])
+    _layer_bar(n(out), ref, msg)
+    for b, (q, p) in enumerate(zip(q_lens, past)):
+        np.testing.assert_allclose(Kw[b, :, p:p + q], rK[b, :, p:p + q], **BF_TOL, err_msg=msg)
+        np.testing.assert_allclose(Vw[b, :, p:p + q], rV[b, :, p:p + q], **BF_TOL, err_msg=msg)
