@@ -12,6 +12,7 @@ length bounds.  The whole decode layer: batch 1-20, group sizes 1-16,
 head_dim 64 / 128, widths, contiguous or paged caches.  Prefill attention:
 chunk lengths (empty ones included), cached prefixes, groups, paging; the
 prefill layer likewise, with widths that take the separate SwiGLU pass.
+QK-norm + RoPE: batch, heads, head_dim 16-256 (both kernels), positions.
 Bar: bf16 allclose(atol 2e-2, rtol 1e-2) against the fp32-accumulated
 oracle (the layer: that bar with the oracle's own accumulation-order slack).
 """
@@ -250,3 +251,38 @@ def test_qwen3_prefill_random(seed):
     for b, (q, p) in enumerate(zip(q_lens, past)):
         np.testing.assert_allclose(Kw[b, :, p:p + q], rK[b, :, p:p + q], **BF_TOL, err_msg=msg)
         np.testing.assert_allclose(Vw[b, :, p:p + q], rV[b, :, p:p + q], **BF_TOL, err_msg=msg)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_qk_norm_rope_random(seed):
+    """Fused QK-norm + RoPE over random batch, head counts, head_dim (the
+    16-byte-lane kernel at 64 / 128 / 256, the pair-per-lane kernel below),
+    capacity and positions (one for the batch or one per sequence): q / k
+    against the oracle, the written cache slot, every other slot untouched."""
+    from ezops import FusedQkNormRopeOp
+
+    rng = np.random.default_rng(8000 + seed)
+    B = int(rng.integers(1, 17))
+    Hkv = int(rng.choice([1, 2, 4, 8]))
+    H = Hkv * int(rng.choice([1, 2, 4, 8]))
+    D = int(rng.choice([16, 32, 64, 128, 256]))
+    S = int(rng.integers(1, 4097))
+    per_seq = bool(rng.integers(0, 2))
+    pos = rng.integers(0, S, size=B).tolist() if per_seq else int(rng.integers(0, S))
+    msg = f"B={B} H={H} Hkv={Hkv} D={D} S={S} pos={pos}"
+    torch.manual_seed(seed)
+    op = FusedQkNormRopeOp(B, H, D, S, pos, backend="hip", num_kv_heads=Hkv)
+    data = list(op.gen_data(DEV))
+    K0, V0 = data[7].clone(), data[8].clone()
+    q_out, k_out = op(*data)
+    p = np.broadcast_to(np.asarray(pos), (B,))
+    rq, rk, _, _ = oracle.qk_norm_rope(*[n(x) for x in data[:7]], n(K0), n(V0), p)
+    np.testing.assert_allclose(n(q_out), rq, **BF_TOL, err_msg=msg)
+    np.testing.assert_allclose(n(k_out), rk, **BF_TOL, err_msg=msg)
+    Kc, Vc = data[7], data[8]
+    for b in range(B):
+        np.testing.assert_allclose(n(Kc[b, :, p[b]]), rk[b], **BF_TOL, err_msg=msg)
+        assert torch.equal(Vc[b, :, p[b]], data[2][b]), msg
+        keep = torch.ones(S, dtype=torch.bool, device=DEV)
+        keep[int(p[b])] = False
+        assert torch.equal(Kc[b][:, keep], K0[b][:, keep]) and torch.equal(Vc[b][:, keep], V0[b][:, keep]), msg
