@@ -13,6 +13,7 @@ head_dim 64 / 128, widths, contiguous or paged caches.  Prefill attention:
 chunk lengths (empty ones included), cached prefixes, groups, paging; the
 prefill layer likewise, with widths that take the separate SwiGLU pass.
 QK-norm + RoPE: batch, heads, head_dim 16-256 (both kernels), positions.
+Row ops: RMSNorm fp32 / bf16, softmax and the full sum over random widths.
 Bar: bf16 allclose(atol 2e-2, rtol 1e-2) against the fp32-accumulated
 oracle (the layer: that bar with the oracle's own accumulation-order slack).
 """
@@ -286,3 +287,36 @@ def test_qk_norm_rope_random(seed):
         keep = torch.ones(S, dtype=torch.bool, device=DEV)
         keep[int(p[b])] = False
         assert torch.equal(Kc[b][:, keep], K0[b][:, keep]) and torch.equal(Vc[b][:, keep], V0[b][:, keep]), msg
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_row_ops_random(seed):
+    """RMSNorm (fp32, and bf16 with a weight), row softmax and the full sum over
+    random row counts and widths (every kernel choice: register-resident rows
+    up to 32768, the looping kernel above, widths that are not a multiple of
+    4 and so take the scalar path) against the oracle with the ops' own checks."""
+    from ezops import ReduceOp, RmsNormOp, SoftmaxOp
+
+    rng = np.random.default_rng(9000 + seed)
+    rows = int(rng.integers(1, 300))
+    dim = int(rng.choice([int(rng.integers(1, 64)), int(rng.integers(64, 4097)), int(rng.integers(4097, 40000))]))
+    msg = f"rows={rows} dim={dim}"
+    torch.manual_seed(seed)
+    op = RmsNormOp(rows, dim, backend="hip")
+    X, Out = op.gen_data(DEV)
+    op(X, Out)
+    assert op.check(Out, torch.from_numpy(oracle.rmsnorm_f32(n(X))).to(DEV)), msg
+    opb = RmsNormOp(rows, dim, backend="hip", dtype=torch.bfloat16, weighted=True)
+    Xb, Wb, Ob = opb.gen_data(DEV)
+    opb(Xb, Wb, Ob)
+    np.testing.assert_allclose(n(Ob), oracle.rmsnorm_bf16(n(Xb), n(Wb)), **BF_TOL, err_msg=msg)
+    ops = SoftmaxOp(rows, dim, backend="hip")
+    Xs, Os = ops.gen_data(DEV)
+    Xs.mul_(4)
+    ops(Xs, Os)
+    assert ops.check(Os, torch.from_numpy(oracle.softmax(n(Xs))).to(DEV)), msg
+    size = int(rng.integers(1, 1 << 22))
+    opr = ReduceOp(size, backend="hip")
+    A, Or = opr.gen_data(DEV)
+    opr(A, Or)
+    assert opr.check(Or, torch.from_numpy(oracle.reduce_sum(n(A))).to(DEV)), (size, Or.item())
