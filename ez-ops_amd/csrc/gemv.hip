@@ -926,8 +926,8 @@ void launch_valu(const LinearArgs& a, hipStream_t s) {
 // projection 17.8 / 18.4 us with 2 / 1; SwiGLU halves them: two gate and
 // two up rows, 32.6 us against 34.5 with one each).  More rows lose at the
 // layer level (config L, batch 1, three alternating runs each: 83.4-85.8 us
-// per layer; four gate + four up rows 86.4-87.1; also eight QKV rows and
-// four down rows 87.6-87.8).
+// per layer; four gate + four up rows 86.4-87.1; four down rows alone
+// 86.4-86.7; with eight QKV rows as well 87.6-87.8).
 constexpr int rows_per_group(int ch, bool silu) { return silu ? (ch <= 2 ? 2 : 1) : (ch <= 2 ? 4 : 2); }
 
 template <int M, int CH, int TPR, bool NORM, bool SILU, bool TAIL>
